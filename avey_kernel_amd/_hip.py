@@ -1,0 +1,165 @@
+"""ctypes binding of libavey_hip.so and the ``avey_kernels::contextualize`` op.
+
+The op is functional: it allocates and returns a fresh output, as the
+reference's ``avey_kernels::mix`` does (``avey_kernels/_triton.py:153-188``),
+and has a fake implementation so fake-tensor tracing and
+``torch.compile(fullgraph=True)`` see an opaque call. Unlike ``mix`` it takes
+the raw ``z_tr`` only: row normalisation happens inside the fused kernel.
+
+Nothing here falls back to another implementation: if the shared library is
+missing or refuses the call, the error surfaces to the caller.
+"""
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libavey_hip.so')
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+ACTIVATION_IDS = {'identity': 0, 'relu': 1, 'relu2': 2, 'silu': 3, 'gelu': 4}
+KERNEL_NAMES = {1: 'fused_mfma', 2: 'generic_valu'}
+
+
+class HipUnavailable(RuntimeError):
+    """libavey_hip.so is missing or cannot be loaded."""
+
+
+class AveyFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ('z_tr', ctypes.c_void_p), ('v', ctypes.c_void_p), ('z_tl', ctypes.c_void_p),
+        ('bias', ctypes.c_void_p), ('valid', ctypes.c_void_p), ('out', ctypes.c_void_p),
+        ('batch', ctypes.c_int64), ('context', ctypes.c_int64), ('features', ctypes.c_int64),
+        ('dtype', ctypes.c_int32), ('causal', ctypes.c_int32), ('normalize', ctypes.c_int32),
+        ('activation', ctypes.c_int32), ('eps', ctypes.c_double), ('norm_eps', ctypes.c_double),
+    ]
+
+
+class AveyFwdPlan(ctypes.Structure):
+    _fields_ = [
+        ('kernel', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
+        ('block_d', ctypes.c_int32), ('threads', ctypes.c_int32), ('waves_per_simd', ctypes.c_int32),
+        ('grid', ctypes.c_int64), ('workspace_bytes', ctypes.c_int64), ('key_tile_steps', ctypes.c_int64),
+    ]
+
+
+# Symbols of include/avey_hip.h with their ctypes signatures.
+EXPORTS = {
+    'avey_fwd': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    'avey_fwd_workspace_bytes': (ctypes.c_int64, [ctypes.POINTER(AveyFwdArgs)]),
+    'avey_fwd_plan': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.POINTER(AveyFwdPlan)]),
+    'avey_key_tile_count': (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                             ctypes.c_int32, ctypes.c_int32]),
+    'avey_device_supported': (ctypes.c_int, [ctypes.c_int]),
+    'avey_status_string': (ctypes.c_char_p, [ctypes.c_int]),
+    'avey_abi_version': (ctypes.c_int, []),
+}
+ABI_VERSION = 1
+
+_lib = None
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def load():
+    """Load libavey_hip.so once; raise HipUnavailable if it is absent or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        raise HipUnavailable(f'{_LIB_PATH} is not built; run `python -m avey_kernel_amd._build`')
+    try:
+        lib = ctypes.CDLL(_LIB_PATH)
+    except OSError as exc:
+        raise HipUnavailable(f'cannot load {_LIB_PATH}: {exc}') from exc
+    for name, (restype, argtypes) in EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if lib.avey_abi_version() != ABI_VERSION:
+        raise HipUnavailable(f'{_LIB_PATH} has ABI {lib.avey_abi_version()}, expected {ABI_VERSION}')
+    _lib = lib
+    return lib
+
+
+def status_string(code):
+    return load().avey_status_string(code).decode()
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def make_args(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation):
+    batch, context, features = z_tr.shape
+    return AveyFwdArgs(
+        _ptr(z_tr), _ptr(v), _ptr(z_tl), _ptr(bias), _ptr(valid), _ptr(out),
+        batch, context, features, DTYPE_CODES[z_tr.dtype], int(bool(causal)), int(bool(normalize)),
+        ACTIVATION_IDS[activation], float(eps), float(norm_eps))
+
+
+def plan(shape, dtype, *, causal, normalize, activation='identity', eps=1e-6, norm_eps=1e-12,
+         has_v=False, has_gate=False, has_bias=False, has_valid=False):
+    """Static tile-table entry for a call, computed on the host (no GPU needed)."""
+    batch, context, features = shape
+    # Distinct non-null placeholders: the plan never dereferences pointers.
+    base = 1 << 40
+    step = 1 << 36
+    args = AveyFwdArgs(base, base + step if has_v else None, base + 2 * step if has_gate else None,
+                       base + 3 * step if has_bias else None, base + 4 * step if has_valid else None,
+                       base + 5 * step, batch, context, features, DTYPE_CODES[dtype], int(causal),
+                       int(normalize), ACTIVATION_IDS[activation], float(eps), float(norm_eps))
+    out = AveyFwdPlan()
+    st = load().avey_fwd_plan(ctypes.byref(args), ctypes.byref(out))
+    if st != 0:
+        raise ValueError(status_string(st))
+    return {
+        'kernel': KERNEL_NAMES.get(out.kernel, str(out.kernel)), 'block_m': out.block_m,
+        'block_n': out.block_n, 'block_d': out.block_d, 'threads': out.threads, 'grid': out.grid,
+        'workspace_bytes': out.workspace_bytes, 'key_tile_steps': out.key_tile_steps,
+    }
+
+
+def device_supported(device):
+    """True if ``device`` (a CUDA/ROCm torch device) is a gfx950 GPU."""
+    idx = torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return bool(load().avey_device_supported(idx))
+
+
+def launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation):
+    """Launch the forward pass into ``out`` on the current stream of z_tr's device."""
+    lib = load()
+    valid_u8 = valid.view(torch.uint8) if valid is not None else None
+    args = make_args(z_tr, v, z_tl, bias, valid_u8, out, eps, norm_eps, causal, normalize, activation)
+    need = lib.avey_fwd_workspace_bytes(ctypes.byref(args))
+    if need < 0:
+        raise ValueError('libavey_hip rejected the arguments')
+    work = torch.empty(max(int(need), 1), dtype=torch.uint8, device=z_tr.device) if need > 0 else None
+    with torch.cuda.device(z_tr.device):
+        stream = torch.cuda.current_stream(z_tr.device).cuda_stream
+        st = lib.avey_fwd(ctypes.byref(args), _ptr(work), int(need), stream)
+    if st < 0:
+        raise ValueError(f'avey_fwd: {status_string(st)}')
+    if st > 0:
+        raise RuntimeError(f'avey_fwd: HIP error {st}: {status_string(st)}')
+    return out
+
+
+@torch.library.custom_op('avey_kernels::contextualize', mutates_args=())
+def contextualize(z_tr: torch.Tensor, v: Optional[torch.Tensor], z_tl: Optional[torch.Tensor],
+                  bias: Optional[torch.Tensor], valid: Optional[torch.Tensor], eps: float,
+                  norm_eps: float, causal: bool, normalize: bool, activation: str) -> torch.Tensor:
+    """out = z_tl * act(mix(z_tr) / den + bias), fused on the GPU; inputs contiguous."""
+    out = torch.empty_like(z_tr, memory_format=torch.contiguous_format)
+    return launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation)
+
+
+@contextualize.register_fake
+def _contextualize_fake(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation):
+    return torch.empty_like(z_tr, memory_format=torch.contiguous_format)

@@ -1,0 +1,206 @@
+// C ABI of libavey_hip.so: argument checks, the static tile table, dispatch.
+#include <math.h>
+#include <string.h>
+
+#include <atomic>
+
+#include "avey_common.h"
+#include "avey_internal.h"
+
+namespace avey {
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_device_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 other
+
+size_t elem_size(int dtype) {
+  switch (dtype) {
+    case AVEY_DTYPE_F32: return 4;
+    case AVEY_DTYPE_F64: return 8;
+    case AVEY_DTYPE_BF16:
+    case AVEY_DTYPE_F16: return 2;
+    default: return 0;
+  }
+}
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+  if (!a || !b) return false;
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bn && y < x + an;
+}
+
+int validate(const avey_fwd_args* a) {
+  if (!a || !a->z_tr || !a->out) return AVEY_ERR_NULL_POINTER;
+  const size_t es = elem_size(a->dtype);
+  if (!es) return AVEY_ERR_DTYPE;
+  if (a->batch < 1 || a->context < 1 || a->features < 1) return AVEY_ERR_SHAPE;
+  // Keep every element offset and the 1-D grid inside 63 / 31 bits.
+  if (a->context > (1 << 24) || a->features > (1 << 24) || a->batch > (1 << 24)) return AVEY_ERR_SHAPE;
+  const double n = (double)a->batch * (double)a->context * (double)a->features;
+  if (n * (double)es > 9.0e18) return AVEY_ERR_SHAPE;
+  if (a->activation < AVEY_ACT_IDENTITY || a->activation > AVEY_ACT_GELU) return AVEY_ERR_ACTIVATION;
+  if (!(isfinite(a->eps) && a->eps > 0) || !(isfinite(a->norm_eps) && a->norm_eps > 0)) return AVEY_ERR_EPS;
+  if ((a->causal != 0 && a->causal != 1) || (a->normalize != 0 && a->normalize != 1)) return AVEY_ERR_FLAGS;
+  const size_t nb = (size_t)n * es;
+  const size_t vb = (size_t)a->context * (size_t)a->context * es;
+  if (overlaps(a->out, nb, a->z_tr, nb) || overlaps(a->out, nb, a->z_tl, nb) || overlaps(a->out, nb, a->v, vb) ||
+      overlaps(a->out, nb, a->bias, (size_t)a->features * es) ||
+      overlaps(a->out, nb, a->valid, (size_t)a->batch * (size_t)a->context))
+    return AVEY_ERR_ALIAS;
+  return AVEY_OK;
+}
+
+// Wave slices of the fused kernel come in multiples of 32 features; only these
+// slice widths are compiled.
+int slice_steps(int64_t D) {
+  const int64_t nk = cdiv(D, 128);
+  if (nk <= 4) return (int)nk;
+  if (nk <= 6) return 6;
+  if (nk <= 8) return 8;
+  return 0;
+}
+
+bool device_ok(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return false;
+  int st = g_device_ok[dev].load(std::memory_order_relaxed);
+  if (st == 0) {
+    hipDeviceProp_t prop;
+    st = 2;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && strncmp(prop.gcnArchName, "gfx950", 6) == 0) st = 1;
+    g_device_ok[dev].store(st, std::memory_order_relaxed);
+  }
+  return st == 1;
+}
+
+}  // namespace
+
+// The static tile table (replaces the reference's runtime autotuner,
+// avey_kernels/_triton.py:131-150). For the fused kernel:
+//   * slice width DS = 32 * ceil(D / 128) features per wave (4 waves cover D);
+//   * BM = 64 query rows when the wave's accumulators fit (DS <= 192), else 32;
+//   * BM halves (down to 16) while the grid would leave CUs of the 256 idle.
+Plan make_plan(const avey_fwd_args& a) {
+  Plan pl{};
+  const bool low = a.dtype == AVEY_DTYPE_BF16 || a.dtype == AVEY_DTYPE_F16;
+  const int nk = slice_steps(a.features);
+  if (low && nk > 0) {
+    pl.kernel = 1;
+    pl.bn = 32;
+    pl.bd = 32 * nk;
+    pl.threads = 256;
+    int bm = nk <= 6 ? 64 : 32;
+    while (bm > 16 && cdiv(a.context, bm) * a.batch < 256) bm /= 2;
+    pl.bm = bm;
+    const int64_t nqt = cdiv(a.context, bm);
+    pl.grid = nqt * a.batch;
+    pl.work_bytes = 0;
+    int64_t steps = 0;
+    for (int64_t qt = 0; qt < nqt; ++qt) steps += key_tiles_for(qt, a.context, bm, 32, a.causal != 0);
+    pl.key_tile_steps = steps * a.batch;
+  } else {
+    pl.kernel = 2;
+    pl.bm = 16;
+    pl.bn = 16;
+    pl.bd = 64;
+    pl.threads = 256;
+    const int64_t nqt = cdiv(a.context, 16);
+    pl.grid = nqt * cdiv(a.features, 64) * a.batch;
+    pl.work_bytes = a.batch * a.context * (a.dtype == AVEY_DTYPE_F64 ? 8 : 4);
+    int64_t steps = 0;
+    for (int64_t qt = 0; qt < nqt; ++qt) steps += key_tiles_for(qt, a.context, 16, 16, a.causal != 0);
+    pl.key_tile_steps = steps * cdiv(a.features, 64) * a.batch;
+  }
+  return pl;
+}
+
+}  // namespace avey
+
+using namespace avey;
+
+extern "C" {
+
+int avey_abi_version(void) { return AVEY_ABI_VERSION; }
+
+const char* avey_status_string(int status) {
+  switch (status) {
+    case AVEY_OK: return "ok";
+    case AVEY_ERR_NULL_POINTER: return "null pointer: args, z_tr and out are required";
+    case AVEY_ERR_SHAPE: return "batch, context and features must be >= 1 and within the supported range";
+    case AVEY_ERR_DTYPE: return "unknown dtype code";
+    case AVEY_ERR_ACTIVATION: return "unknown activation id";
+    case AVEY_ERR_EPS: return "eps and norm_eps must be finite and positive";
+    case AVEY_ERR_WORKSPACE: return "workspace smaller than avey_fwd_workspace_bytes";
+    case AVEY_ERR_DEVICE: return "current HIP device is not a gfx950 (MI355X) GPU";
+    case AVEY_ERR_FLAGS: return "causal and normalize must be 0 or 1";
+    case AVEY_ERR_ALIAS: return "out overlaps an input buffer";
+    default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+  }
+}
+
+int64_t avey_key_tile_count(int64_t query_tile, int64_t context, int32_t block_m, int32_t block_n, int32_t causal,
+                            int32_t skip) {
+  if (query_tile < 0 || context < 1 || block_m < 1 || block_n < 1) return -1;
+  if (query_tile * (int64_t)block_m >= context) return -1;
+  return key_tiles_for(query_tile, context, block_m, block_n, causal != 0 && skip != 0);
+}
+
+int64_t avey_fwd_workspace_bytes(const avey_fwd_args* args) {
+  if (validate(args) != AVEY_OK) return -1;
+  return make_plan(*args).work_bytes;
+}
+
+int avey_fwd_plan(const avey_fwd_args* args, avey_fwd_plan_t* out) {
+  const int st = validate(args);
+  if (st != AVEY_OK) return st;
+  if (!out) return AVEY_ERR_NULL_POINTER;
+  const Plan pl = make_plan(*args);
+  out->kernel = pl.kernel;
+  out->block_m = pl.bm;
+  out->block_n = pl.bn;
+  out->block_d = pl.bd;
+  out->threads = pl.threads;
+  out->waves_per_simd = 1;
+  out->grid = pl.grid;
+  out->workspace_bytes = pl.work_bytes;
+  out->key_tile_steps = pl.key_tile_steps;
+  return AVEY_OK;
+}
+
+int avey_device_supported(int device) { return device_ok(device) ? 1 : 0; }
+
+int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = validate(a);
+  if (st != AVEY_OK) return st;
+  const Plan pl = make_plan(*a);
+  if (pl.work_bytes > 0 && (!workspace || workspace_bytes < (size_t)pl.work_bytes)) return AVEY_ERR_WORKSPACE;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (!device_ok(dev)) return AVEY_ERR_DEVICE;
+
+  FwdParams p{};
+  p.z = a->z_tr;
+  p.v = a->v;
+  p.gate = a->z_tl;
+  p.bias = a->bias;
+  p.valid = a->valid;
+  p.out = a->out;
+  p.work = workspace;
+  p.B = a->batch;
+  p.C = a->context;
+  p.D = a->features;
+  p.causal = a->causal;
+  p.normalize = a->normalize;
+  p.act = a->activation;
+  p.eps = a->eps;
+  p.norm_eps = a->norm_eps;
+  const auto al16 = [](const void* x) { return x == nullptr || ((uintptr_t)x & 15) == 0; };
+  p.aligned = (a->features % 8 == 0) && al16(a->z_tr) && al16(a->z_tl) && al16(a->out);
+
+  hipStream_t s = (hipStream_t)stream;
+  e = pl.kernel == 1 ? launch_fused(p, a->dtype, pl, s) : launch_generic(p, a->dtype, pl, s);
+  return e == hipSuccess ? AVEY_OK : (int)e;
+}
+
+}  // extern "C"

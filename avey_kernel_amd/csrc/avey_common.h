@@ -1,0 +1,100 @@
+// Device helpers shared by the contextualizer kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "avey_hip.h"
+
+namespace avey {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Element-type traits: storage type, fp conversion, accumulator type.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  typedef float acc;
+  __device__ static float to_acc(float x) { return x; }
+  __device__ static float from_acc(float x) { return x; }
+};
+template <> struct Elem<double> {
+  typedef double acc;
+  __device__ static double to_acc(double x) { return x; }
+  __device__ static double from_acc(double x) { return x; }
+};
+template <> struct Elem<__bf16> {
+  typedef float acc;
+  __device__ static float to_acc(__bf16 x) { return (float)x; }
+  // Round to nearest even (v_cvt_pk_bf16_f32), the same rounding as torch's .to(bfloat16).
+  __device__ static __bf16 from_acc(float x) { return (__bf16)x; }
+};
+template <> struct Elem<_Float16> {
+  typedef float acc;
+  __device__ static float to_acc(_Float16 x) { return (float)x; }
+  __device__ static _Float16 from_acc(float x) { return (_Float16)x; }
+};
+
+// Activations of avey_kernels/ops.py:49-58. GELU is the tanh form.
+template <typename A>
+__device__ __forceinline__ A activate(A x, int act) {
+  switch (act) {
+    case AVEY_ACT_RELU: return x > A(0) ? x : A(0);
+    case AVEY_ACT_RELU2: { A r = x > A(0) ? x : A(0); return r * r; }
+    case AVEY_ACT_SILU: {
+      // x * sigmoid(x), with exp evaluated on -|x| so it cannot overflow.
+      A e = exp(-fabs(x));
+      A s = x >= A(0) ? A(1) / (A(1) + e) : e / (A(1) + e);
+      return x * s;
+    }
+    case AVEY_ACT_GELU: {
+      const A k = A(0.7978845608028654);  // sqrt(2 / pi)
+      A t = k * (x + A(0.044715) * x * x * x);
+      return A(0.5) * x * (A(1) + tanh(t));
+    }
+    default: return x;
+  }
+}
+template <>
+__device__ __forceinline__ float activate<float>(float x, int act) {
+  switch (act) {
+    case AVEY_ACT_RELU: return x > 0.f ? x : 0.f;
+    case AVEY_ACT_RELU2: { float r = x > 0.f ? x : 0.f; return r * r; }
+    case AVEY_ACT_SILU: {
+      float e = expf(-fabsf(x));
+      float s = x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+      return x * s;
+    }
+    case AVEY_ACT_GELU: {
+      float t = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+      return 0.5f * x * (1.f + tanhf(t));
+    }
+    default: return x;
+  }
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Key tiles a query tile visits. Causal skipping keeps the tile holding the
+// diagonal and drops every tile that starts after the block's last query
+// (the reference rule, avey_kernels/_triton.py:38-50).
+__host__ __device__ __forceinline__ int64_t key_tiles_for(int64_t query_tile, int64_t context, int64_t bm,
+                                                          int64_t bn, bool causal_skip) {
+  if (context <= bn) return 1;
+  if (causal_skip) {
+    int64_t end = (query_tile + 1) * bm;
+    if (end > context) end = context;
+    return cdiv(end, bn);
+  }
+  return cdiv(context, bn);
+}
+
+}  // namespace avey

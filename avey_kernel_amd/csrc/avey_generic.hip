@@ -1,0 +1,164 @@
+// Generic contextualizer kernels (VALU, any element type).
+//
+// Used for fp32 and fp64 inputs and for feature widths beyond the fused MFMA
+// kernel's register budget. Arithmetic follows the reference's eager path
+// (avey_kernels/ops.py:61-91) in the accumulation type of Elem<T> (fp32, or fp64
+// for fp64 inputs): inverse row norms first, then per output tile the
+// similarity of every allowed (query, key) pair, the learned weight, masks, the
+// signed row sum and the mixing sum, then the fused epilogue.
+#include "avey_common.h"
+#include "avey_internal.h"
+
+namespace avey {
+
+// inv[b*C + j] = 1 / max(||z_j||_2, norm_eps); padded rows count as zero rows
+// (ops.py:64-68). One wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void row_inv_norm_kernel(const T* __restrict__ z, const uint8_t* __restrict__ valid,
+                                                           typename Elem<T>::acc* __restrict__ inv, int64_t rows,
+                                                           int64_t D, double norm_eps) {
+  typedef typename Elem<T>::acc A;
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (row >= rows) return;
+  A ss = 0;
+  if (!valid || valid[row]) {
+    const T* zr = z + row * D;
+    for (int64_t f = lane; f < D; f += 64) {
+      A x = Elem<T>::to_acc(zr[f]);
+      ss += x * x;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  if (lane == 0) {
+    A n = sqrt(ss);
+    A e = (A)norm_eps;
+    inv[row] = A(1) / (n > e ? n : e);
+  }
+}
+
+// One workgroup per (batch, 16-query tile, 64-feature output tile), numbered on a
+// 1-D grid. Key tiles of 16 rows; the similarity tile is recomputed for every
+// output tile.
+template <typename T>
+__global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
+  typedef typename Elem<T>::acc A;
+  constexpr int BQ = 16, BK = 16, BF = 64, DC = 64;
+  __shared__ A qs[BQ][DC + 1];
+  __shared__ A ks[BK][DC + 1];
+  __shared__ A ss[BQ][BK + 1];
+  __shared__ A kf[BK][BF + 1];
+  __shared__ A den_s[BQ];
+  __shared__ A rq[BQ];
+
+  const int t = threadIdx.x;
+  const int64_t C = p.C, D = p.D;
+  const int64_t nft = cdiv(D, BF), nqt = cdiv(C, BQ);
+  const int64_t ft = (int64_t)blockIdx.x % nft;
+  const int64_t qt = ((int64_t)blockIdx.x / nft) % nqt;
+  const int64_t b = (int64_t)blockIdx.x / nft / nqt;
+  const int64_t q0 = qt * BQ, f0 = ft * BF;
+  const T* zb = (const T*)p.z + b * C * D;
+  const uint8_t* vb = p.valid ? p.valid + b * C : nullptr;
+  const A* inv = (const A*)p.work + b * C;
+  const T* vw = (const T*)p.v;
+
+  const int si = t / BK, sj = t % BK;       // similarity element owned
+  const int oi = t / 16, of = (t % 16) * 4;  // output row / first feature owned
+  A acc[4] = {A(0), A(0), A(0), A(0)};
+  if (t < BQ) {
+    den_s[t] = A(0);
+    const int64_t q = q0 + t;
+    rq[t] = q < C ? inv[q] : A(0);
+  }
+  auto row_ok = [&](int64_t r) { return r < C && (!vb || vb[r]); };
+
+  const int64_t nkt = key_tiles_for(qt, C, BQ, BK, p.causal != 0);
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = kt * BK;
+    A s = A(0);
+    for (int64_t d0 = 0; d0 < D; d0 += DC) {
+      __syncthreads();
+      for (int e = t; e < BQ * DC; e += 256) {
+        const int r = e / DC, c = e % DC;
+        const int64_t f = d0 + c;
+        const int64_t q = q0 + r, k = k0 + r;
+        qs[r][c] = (f < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * D + f]) : A(0);
+        ks[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * D + f]) : A(0);
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int c = 0; c < DC; ++c) s += qs[si][c] * ks[sj][c];
+    }
+    {
+      const int64_t q = q0 + si, k = k0 + sj;
+      const bool allowed = row_ok(q) && row_ok(k) && (!p.causal || k <= q);
+      if (allowed) {
+        s = s * rq[si] * inv[k];
+        if (vw) s *= Elem<T>::to_acc(vw[q * C + k]);
+      } else {
+        s = A(0);
+      }
+      ss[si][sj] = s;
+    }
+    for (int e = t; e < BK * BF; e += 256) {
+      const int r = e / BF, c = e % BF;
+      const int64_t k = k0 + r, f = f0 + c;
+      kf[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * D + f]) : A(0);
+    }
+    __syncthreads();
+    if (p.normalize && t < BQ) {
+      A d = A(0);
+      for (int j = 0; j < BK; ++j) d += ss[t][j];
+      den_s[t] += d;
+    }
+#pragma unroll 4
+    for (int j = 0; j < BK; ++j) {
+      const A sv = ss[oi][j];
+      for (int u = 0; u < 4; ++u) acc[u] += sv * kf[j][of + u];
+    }
+  }
+  __syncthreads();
+
+  const int64_t q = q0 + oi;
+  if (q >= C) return;
+  const bool qv = !vb || vb[q];
+  const T* bias = (const T*)p.bias;
+  const T* gate = (const T*)p.gate;
+  T* out = (T*)p.out + (b * C + q) * D;
+  const A dd = p.normalize ? den_s[oi] + (A)p.eps : A(1);
+  for (int u = 0; u < 4; ++u) {
+    const int64_t f = f0 + of + u;
+    if (f >= D) break;
+    A y = acc[u];
+    if (p.normalize) y = y / dd;
+    if (bias) y += Elem<T>::to_acc(bias[f]);
+    y = activate<A>(y, p.act);
+    if (gate) y *= qv ? Elem<T>::to_acc(gate[(b * C + q) * D + f]) : A(0);
+    out[f] = Elem<T>::from_acc(qv ? y : A(0));
+  }
+}
+
+template <typename T>
+static hipError_t launch_generic_t(const FwdParams& p, hipStream_t s) {
+  const int64_t rows = p.B * p.C;
+  row_inv_norm_kernel<T><<<dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s>>>(
+      (const T*)p.z, p.valid, (typename Elem<T>::acc*)p.work, rows, p.D, p.norm_eps);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t grid = cdiv(p.C, 16) * cdiv(p.D, 64) * p.B;
+  generic_fwd_kernel<T><<<dim3((unsigned)grid), dim3(256), 0, s>>>(p);
+  return hipGetLastError();
+}
+
+hipError_t launch_generic(const FwdParams& p, int dtype, const Plan&, hipStream_t s) {
+  switch (dtype) {
+    case AVEY_DTYPE_F32: return launch_generic_t<float>(p, s);
+    case AVEY_DTYPE_F64: return launch_generic_t<double>(p, s);
+    case AVEY_DTYPE_BF16: return launch_generic_t<__bf16>(p, s);
+    case AVEY_DTYPE_F16: return launch_generic_t<_Float16>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace avey

@@ -1,0 +1,41 @@
+// Internal launch interface between the C ABI (avey_capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "avey_hip.h"
+
+namespace avey {
+
+// Everything a kernel needs, by value. Pointers are device pointers.
+struct FwdParams {
+  const void* z;        // z_tr [B][C][D]
+  const void* v;        // [C][C] or null
+  const void* gate;     // z_tl [B][C][D] or null
+  const void* bias;     // [D] or null
+  const uint8_t* valid; // [B][C] or null
+  void* out;            // [B][C][D]
+  void* work;           // scratch (generic path: per-row inverse norms)
+  int64_t B, C, D;
+  int32_t causal, normalize, act;
+  int32_t aligned;      // D % 8 == 0 and z/gate/out 16-byte aligned, bias 8-byte aligned
+  double eps, norm_eps;
+};
+
+// Static tile table entry chosen on the host.
+struct Plan {
+  int kernel;     // 1 fused MFMA, 2 generic
+  int bm, bn, bd; // query rows per WG, keys per step, features per wave slice / output tile
+  int threads;
+  int64_t grid;
+  int64_t work_bytes;
+  int64_t key_tile_steps;
+};
+
+Plan make_plan(const avey_fwd_args& a);
+
+hipError_t launch_generic(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s);
+hipError_t launch_fused(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s);
+
+}  // namespace avey

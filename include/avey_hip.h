@@ -1,0 +1,130 @@
+/*
+ * avey_hip.h -- C ABI of libavey_hip.so, the MI355X (gfx950) forward
+ * contextualizer for Avey and Avey-B.
+ *
+ * The library replaces the reference's device path for this op
+ * (HusamettinYilmazz/avey_kernel):
+ *   - avey_fwd            replaces the custom op `mix` and its launch of the
+ *                         Triton kernel `_mix_kernel` (avey_kernels/_triton.py:153-188,
+ *                         kernel at :53-128) together with the separate
+ *                         F.normalize pass in `_dispatch` (avey_kernels/ops.py:107-108):
+ *                         one call computes out = gate * act(mix / den + bias).
+ *   - avey_fwd_plan       replaces the Triton autotuner and its 84-entry
+ *                         candidate table (avey_kernels/_triton.py:131-150) with a
+ *                         static, documented tile table; host-only, no GPU needed.
+ *   - avey_key_tile_count replaces `_key_tile_count` (avey_kernels/_triton.py:38-50),
+ *                         the causal tile-skip rule; host-only.
+ *   - avey_fwd_workspace_bytes, avey_status_string, avey_abi_version,
+ *     avey_device_supported: plumbing for the Python binding
+ *     (avey_kernel_amd/_hip.py), no reference counterpart beyond the op's
+ *     argument checks (avey_kernels/_triton.py:165-166).
+ *
+ * Conventions
+ *   - All tensor pointers are device pointers owned by the caller. The
+ *     library never allocates, frees or keeps pointers after a call returns.
+ *   - z_tr, z_tl, out: [batch][context][features], row-major, contiguous.
+ *     v: [context][context] indexed [query][key], shared by the batch.
+ *     bias: [features]. valid: [batch][context] bytes (0 = padded row).
+ *     z_tr, z_tl, v, bias and out share one element type (ops.py:39-43).
+ *   - Launches are asynchronous on the caller's HIP stream; no host sync.
+ *   - Errors are returned as status codes; nothing throws or aborts across
+ *     the ABI. Negative = invalid argument, positive = hipError_t value.
+ */
+#ifndef AVEY_HIP_H
+#define AVEY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AVEY_ABI_VERSION 1
+
+/* Element type of z_tr / z_tl / v / bias / out. */
+enum avey_dtype {
+  AVEY_DTYPE_F32 = 0,
+  AVEY_DTYPE_F16 = 1,
+  AVEY_DTYPE_BF16 = 2,
+  AVEY_DTYPE_F64 = 3,
+};
+
+/* Activation ids, same numbering as the reference's kernel (avey_kernels/_triton.py:169). */
+enum avey_activation {
+  AVEY_ACT_IDENTITY = 0,
+  AVEY_ACT_RELU = 1,
+  AVEY_ACT_RELU2 = 2,
+  AVEY_ACT_SILU = 3,
+  AVEY_ACT_GELU = 4, /* tanh approximation, ops.py:57 */
+};
+
+enum avey_status {
+  AVEY_OK = 0,
+  AVEY_ERR_NULL_POINTER = -1,     /* args, z_tr or out is NULL */
+  AVEY_ERR_SHAPE = -2,            /* batch, context or features < 1, or too large */
+  AVEY_ERR_DTYPE = -3,            /* unknown dtype code */
+  AVEY_ERR_ACTIVATION = -4,       /* unknown activation id */
+  AVEY_ERR_EPS = -5,              /* eps or norm_eps not finite and > 0 */
+  AVEY_ERR_WORKSPACE = -6,        /* workspace smaller than avey_fwd_workspace_bytes */
+  AVEY_ERR_DEVICE = -7,           /* current device is not gfx950 */
+  AVEY_ERR_FLAGS = -8,            /* causal / normalize not 0 or 1 */
+  AVEY_ERR_ALIAS = -9,            /* out overlaps an input */
+};
+
+typedef struct avey_fwd_args {
+  const void* z_tr;     /* required */
+  const void* v;        /* optional (NULL: no learned weights, Avey-B) */
+  const void* z_tl;     /* optional gate */
+  const void* bias;     /* optional */
+  const uint8_t* valid; /* optional key/query padding mask */
+  void* out;            /* required */
+  int64_t batch;
+  int64_t context;      /* C: tokens (query and key positions) */
+  int64_t features;     /* d': feature width */
+  int32_t dtype;        /* enum avey_dtype */
+  int32_t causal;       /* 1: keys j <= query i only (diagonal kept) */
+  int32_t normalize;    /* 1: divide by the signed row sum + eps (Avey-B) */
+  int32_t activation;   /* enum avey_activation */
+  double eps;           /* denominator epsilon (used when normalize = 1) */
+  double norm_eps;      /* F.normalize clamp of the row norm */
+} avey_fwd_args;
+
+/* Kernel choice and launch geometry for one call; filled by avey_fwd_plan. */
+typedef struct avey_fwd_plan_t {
+  int32_t kernel;        /* 1 = fused MFMA (bf16/fp16), 2 = generic VALU (fp32/fp64/wide) */
+  int32_t block_m;       /* query rows per workgroup */
+  int32_t block_n;       /* key rows per pipeline step */
+  int32_t block_d;       /* features per output tile (generic) or per wave slice (MFMA) */
+  int32_t threads;       /* threads per workgroup */
+  int32_t waves_per_simd;
+  int64_t grid;          /* workgroups launched by the main kernel */
+  int64_t workspace_bytes;
+  int64_t key_tile_steps;   /* sum over workgroups of key tiles visited */
+} avey_fwd_plan_t;
+
+/* Launch the forward contextualizer on `stream` (a hipStream_t; NULL = default stream). */
+int avey_fwd(const avey_fwd_args* args, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device scratch bytes avey_fwd needs for these arguments (0 when none). Host-only. */
+int64_t avey_fwd_workspace_bytes(const avey_fwd_args* args);
+
+/* Describe the launch avey_fwd would make, without touching a GPU. Returns a status. */
+int avey_fwd_plan(const avey_fwd_args* args, avey_fwd_plan_t* plan);
+
+/* Key tiles visited by query tile `query_tile` (the causal skip rule keeps the
+ * diagonal tile). Host-only. Returns -1 on invalid input. */
+int64_t avey_key_tile_count(int64_t query_tile, int64_t context, int32_t block_m, int32_t block_n,
+                            int32_t causal, int32_t skip);
+
+/* 1 if `device` is a gfx950 GPU this library can run on, else 0. */
+int avey_device_supported(int device);
+
+const char* avey_status_string(int status);
+int avey_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AVEY_HIP_H */

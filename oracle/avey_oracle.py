@@ -1,0 +1,169 @@
+"""CPU oracle for the Avey / Avey-B forward contextualizer (numpy).
+
+TEST INFRASTRUCTURE ONLY. This module is the parity checker. Only code under
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it. The product package ``avey_kernel_amd`` never
+imports, links or calls anything under ``oracle/``.
+
+It restates the reference's eager algorithm (``avey_kernels/ops.py:61-91``)
+step for step in numpy, at a selectable accumulation precision:
+
+* ``acc=np.float32`` follows the reference's own arithmetic type for
+  fp16/bf16/fp32 inputs (``ops.py:62-63``: low-precision input is upcast to
+  fp32, fp64 stays fp64);
+* ``acc=np.float64`` is the high-precision oracle used to bound the error of
+  both the reference-precision path and the HIP kernels.
+
+Inputs are numpy arrays. bf16/fp16 tensors must be upcast to fp32 by the
+caller first (exact), e.g. ``t.float().numpy()``; numpy has no bfloat16.
+
+Pinning (each check lives in ``tests/test_oracle.py``):
+
+* ``activate``: closed forms of ReLU / ReLU^2 / SiLU / tanh-GELU at chosen
+  points, and ``torch.nn.functional`` on random points.
+* ``contextualize``: the reference's hand-computed known answers
+  (``tests/test_contextualizer.py:13-39``, ``tests/test_profiling.py:46-61``,
+  ``tests/test_triton.py:251-258``), transcribed into
+  ``tests/golden/kats.json``; the independent C restatement
+  ``oracle/avey_oracle.c`` (a per-query streaming loop, no N x N matrix) on
+  random inputs with every flag combination; invariants (causal output rows
+  depend only on earlier rows; permuting keys in the bidirectional case
+  leaves outputs unchanged; NaN in masked rows never reaches valid outputs).
+* ``key_tile_count``: the reference's closed-form table
+  (``tests/test_causal_skip.py:52-60``) and a brute-force count of tiles
+  holding at least one allowed (query, key) pair.
+"""
+
+import math
+
+import numpy as np
+
+ACTIVATIONS = ('identity', 'relu', 'relu2', 'silu', 'gelu')
+
+# sqrt(2/pi), the tanh-GELU constant (ops.py:57 selects PyTorch's tanh form).
+_GELU_K = math.sqrt(2.0 / math.pi)
+
+
+def _sigmoid(x):
+    # Evaluated without overflow for large |x|: exp of a non-positive number only.
+    e = np.exp(-np.abs(x))
+    return np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def activate(x, activation):
+    """Elementwise activation, ``avey_kernels/ops.py:49-58``.
+
+    identity; relu = max(x, 0); relu2 = max(x, 0)^2; silu = x * sigmoid(x);
+    gelu = 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 x^3))).
+    """
+    if activation == 'identity':
+        return x
+    if activation == 'relu':
+        return np.maximum(x, 0)
+    if activation == 'relu2':
+        r = np.maximum(x, 0)
+        return r * r
+    if activation == 'silu':
+        return x * _sigmoid(x)
+    if activation == 'gelu':
+        inner = _GELU_K * (x + 0.044715 * x * x * x)
+        return 0.5 * x * (1.0 + np.tanh(inner))
+    raise ValueError(f'unknown activation {activation!r}')
+
+
+def normalize_rows(z, norm_eps):
+    """F.normalize along the feature axis: z / max(||z||_2, norm_eps) (ops.py:68)."""
+    norms = np.sqrt(np.sum(z * z, axis=-1, keepdims=True))
+    return z / np.maximum(norms, z.dtype.type(norm_eps))
+
+
+def contextualize(z_tr, v=None, z_tl=None, bias=None, valid=None, *, eps, norm_eps,
+                  causal, normalize, activation, acc=np.float64):
+    """Restatement of ``_reference`` (``avey_kernels/ops.py:61-91``).
+
+    Shapes: z_tr, z_tl [B, C, D]; v [C, C] indexed [query, key] and shared over
+    the batch (``ops.py:4-6``); bias [D]; valid bool [B, C]. Returns the
+    unrounded result in ``acc`` precision (the reference's final cast to the
+    input dtype, ``ops.py:91``, is left to the caller).
+    """
+    z = np.array(z_tr, dtype=acc, copy=True)
+    bsz, c, d = z.shape
+    if valid is not None:
+        valid = np.asarray(valid, dtype=bool)
+        # ops.py:64-67 -- select zeros into padded rows before any arithmetic,
+        # so NaN in padding cannot propagate.
+        z = np.where(valid[:, :, None], z, acc(0))
+    zn = normalize_rows(z, norm_eps)  # ops.py:68
+    # ops.py:69 -- cosine similarity, S[b, i, j] = zn_i . zn_j.
+    s = np.matmul(zn, np.swapaxes(zn, 1, 2))
+    if v is not None:
+        # ops.py:70-71 -- learned mixing weights, [query, key].
+        s = s * np.asarray(v, dtype=acc)[None]
+    if causal:
+        # ops.py:72-75 -- keys after the query are dropped; the diagonal stays.
+        allowed = np.tril(np.ones((c, c), dtype=bool))
+        s = np.where(allowed[None], s, acc(0))
+    if valid is not None:
+        # ops.py:76-77 -- padded keys contribute nothing.
+        s = np.where(valid[:, None, :], s, acc(0))
+    # ops.py:78 -- mixing with the unnormalised rows.
+    num = np.matmul(s, z)
+    if normalize:
+        # ops.py:79-80 -- signed row sum plus eps; no clamp, abs or softmax.
+        num = num / (np.sum(s, axis=-1, keepdims=True) + acc(eps))
+    if bias is not None:
+        num = num + np.asarray(bias, dtype=acc)  # ops.py:81-82
+    out = activate(num, activation)  # ops.py:83
+    if z_tl is not None:
+        gate = np.asarray(z_tl, dtype=acc)
+        if valid is not None:
+            gate = np.where(valid[:, :, None], gate, acc(0))  # ops.py:86-87
+        out = out * gate  # ops.py:88
+    if valid is not None:
+        out = np.where(valid[:, :, None], out, acc(0))  # ops.py:89-90
+    return out.astype(acc, copy=False)
+
+
+def avey(z_tr, v, *, z_tl=None, bias=None, valid=None, causal=True, norm_eps=1e-12,
+         activation='identity', acc=np.float64):
+    """Avey defaults, ``avey_kernels/ops.py:117-133``: eps=1e-6 (unused, normalize off)."""
+    return contextualize(z_tr, v, z_tl, bias, valid, eps=1e-6, norm_eps=norm_eps,
+                         causal=causal, normalize=False, activation=activation, acc=acc)
+
+
+def avey_b(z_tr, *, z_tl=None, bias=None, valid=None, eps=1e-6, norm_eps=1e-12,
+           activation='identity', acc=np.float64):
+    """Avey-B defaults, ``avey_kernels/ops.py:136-147``: no V, bidirectional, normalised."""
+    return contextualize(z_tr, None, z_tl, bias, valid, eps=eps, norm_eps=norm_eps,
+                         causal=False, normalize=True, activation=activation, acc=acc)
+
+
+def key_tile_count(query_tile, c, bm, bn, causal, skip=True):
+    """Key tiles a query tile visits, ``avey_kernels/_triton.py:38-50``.
+
+    With causal skipping the tile holding the diagonal is kept and every
+    tile strictly after the last query of the block is dropped.
+    """
+    if c <= bn:
+        return 1
+    if causal and skip:
+        query_end = min((query_tile + 1) * bm, c)
+        return -(-query_end // bn)
+    return -(-c // bn)
+
+
+def row_condition(z_tr, valid=None, *, eps=1e-6, norm_eps=1e-12):
+    """Per-row conditioning of the Avey-B denominator, sum|S_ij| / |sum S_ij + eps|.
+
+    Used only to report how much a row amplifies rounding (no reference
+    counterpart; derived from ops.py:79-80).
+    """
+    z = np.array(z_tr, dtype=np.float64, copy=True)
+    if valid is not None:
+        valid = np.asarray(valid, dtype=bool)
+        z = np.where(valid[:, :, None], z, 0.0)
+    zn = z / np.maximum(np.sqrt(np.sum(z * z, -1, keepdims=True)), norm_eps)
+    s = np.matmul(zn, np.swapaxes(zn, 1, 2))
+    if valid is not None:
+        s = np.where(valid[:, None, :], s, 0.0)
+    return np.sum(np.abs(s), -1) / np.abs(np.sum(s, -1) + eps)

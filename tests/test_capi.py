@@ -1,0 +1,106 @@
+"""The C ABI of libavey_hip.so, exercised without a GPU.
+
+Checks that the library loads, exports exactly what include/avey_hip.h
+declares, rejects bad arguments with the documented status codes before
+touching a device, and that the host-only planning functions follow the
+reference's causal tile rule (tests/test_causal_skip.py:52-60).
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from avey_kernel_amd import _hip
+from conftest import REPO, load_kats
+
+HEADER = os.path.join(REPO, 'include', 'avey_hip.h')
+
+
+def _lib():
+    if not os.path.exists(_hip.library_path()):
+        from avey_kernel_amd import _build
+        _build.build(verbose=False)
+    return _hip.load()
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return set(re.findall(r'\b(avey_[a-z_0-9]+)\s*\(', text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    declared = _declared_functions()
+    assert declared == set(_hip.EXPORTS), declared ^ set(_hip.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.avey_abi_version() == 1
+
+
+def _args(**over):
+    base = dict(z_tr=1 << 40, v=None, z_tl=None, bias=None, valid=None, out=(1 << 40) + (1 << 36),
+                batch=2, context=35, features=37, dtype=2, causal=1, normalize=0, activation=0, eps=1e-6,
+                norm_eps=1e-12)
+    base.update(over)
+    return _hip.AveyFwdArgs(*[base[f] for f, _ in _hip.AveyFwdArgs._fields_])
+
+
+@pytest.mark.parametrize('over,code', [
+    (dict(z_tr=None), -1), (dict(out=None), -1),
+    (dict(batch=0), -2), (dict(context=0), -2), (dict(features=-3), -2),
+    (dict(dtype=9), -3), (dict(activation=5), -4), (dict(activation=-1), -4),
+    (dict(eps=0.0), -5), (dict(norm_eps=float('nan')), -5), (dict(eps=float('inf')), -5),
+    (dict(causal=2), -8), (dict(normalize=-1), -8),
+    (dict(out=(1 << 40) + 64), -9),
+])
+def test_argument_errors_return_status_before_any_device_work(over, code):
+    lib = _lib()
+    args = _args(**over)
+    assert lib.avey_fwd(ctypes.byref(args), None, 0, None) == code
+    assert lib.avey_fwd_plan(ctypes.byref(args), ctypes.byref(_hip.AveyFwdPlan())) == code
+    assert lib.avey_fwd_workspace_bytes(ctypes.byref(args)) == -1
+    assert lib.avey_status_string(code).decode() not in ('', 'unknown status')
+
+
+def test_null_args_pointer():
+    lib = _lib()
+    assert lib.avey_fwd(None, None, 0, None) == -1
+
+
+def test_key_tile_count_follows_reference_table():
+    lib = _lib()
+    for case in load_kats()['causal_tile_counts']['cases']:
+        c, bm, bn = case['c'], case['bm'], case['bn']
+        n = len(case['expected'])
+        assert [lib.avey_key_tile_count(q, c, bm, bn, 1, 1) for q in range(n)] == case['expected']
+        full = [-(-c // bn)] * n
+        assert [lib.avey_key_tile_count(q, c, bm, bn, 1, 0) for q in range(n)] == full
+        assert [lib.avey_key_tile_count(q, c, bm, bn, 0, 1) for q in range(n)] == full
+    assert lib.avey_key_tile_count(5, 64, 16, 16, 1, 1) == -1  # tile past the context
+
+
+def test_static_tile_table():
+    _lib()
+    # Headline config: bf16, causal, D=768 -> fused MFMA kernel, 4 x 192-feature wave slices.
+    p = _hip.plan((16, 256, 768), torch.bfloat16, causal=True, normalize=False, has_v=True, has_gate=True,
+                  has_bias=True)
+    assert p['kernel'] == 'fused_mfma' and p['block_d'] == 192 and p['block_n'] == 32
+    assert p['grid'] >= 256 and p['workspace_bytes'] == 0
+    # The grid keeps every CU of the 256 busy where the shape allows it.
+    for shape in ((32, 512, 768), (4, 2048, 1024), (256, 128, 512)):
+        q = _hip.plan(shape, torch.bfloat16, causal=False, normalize=True)
+        assert q['kernel'] == 'fused_mfma' and q['grid'] >= 256
+    # Causal skipping visits about half the key tiles of the full traversal.
+    full = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=False, normalize=False)
+    half = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=True, normalize=False)
+    assert half['block_m'] == full['block_m']
+    assert abs(half['key_tile_steps'] / full['key_tile_steps'] - 0.5) < 0.02
+    # fp32 / fp64 and very wide features take the generic kernel, which needs a workspace.
+    for dt in (torch.float32, torch.float64):
+        g = _hip.plan((2, 64, 64), dt, causal=True, normalize=False)
+        assert g['kernel'] == 'generic_valu' and g['workspace_bytes'] == 2 * 64 * (8 if dt == torch.float64 else 4)
+    assert _hip.plan((1, 8, 4096), torch.bfloat16, causal=False, normalize=True)['kernel'] == 'generic_valu'

@@ -1,0 +1,272 @@
+"""Parity of the HIP kernels against the CPU oracle (needs a gfx950 GPU).
+
+Tolerances (compared with the fp64 oracle on identical inputs):
+  fp64 1e-10, fp32 1e-5 (rtol = atol, the reference's fp32 bound,
+  tests/test_triton.py:68), fp16 5e-3, bf16 2e-2 (rtol = atol; the build's
+  stated bf16 bound). bf16 cases also report max-abs and the row-normwise
+  relative error, which must stay <= 1e-2.
+
+Cases follow the reference's tail shapes and flag combinations
+(tests/test_triton.py:215-249, tests/test_causal_skip.py:80-105): contexts that
+cross query / key tile edges, feature widths that cross slice edges, NaN in
+padded rows, every activation; then the five benchmark configurations at full
+size, size-independent properties (bitwise determinism, causal rows blind to
+the future) and HIP-graph replay.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from avey_kernel_amd import _hip, avey, avey_b
+from avey_kernel_amd import workloads as wl
+from conftest import gpu_available, load_kats
+from oracle import avey_oracle as orc
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason='needs a gfx950 GPU')]
+
+TOL = {torch.float64: 1e-10, torch.float32: 1e-5, torch.float16: 5e-3, torch.bfloat16: 2e-2}
+DEV = 'cuda'
+
+
+def _np(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def _oracle(z, v, gate, bias, valid, *, eps, causal, normalize, act, acc=np.float64):
+    return orc.contextualize(_np(z), _np(v), _np(gate), _np(bias), None if valid is None else valid.cpu().numpy(),
+                             eps=eps, norm_eps=1e-12, causal=causal, normalize=normalize, activation=act, acc=acc)
+
+
+def _fused(z, v, gate, bias, valid, *, eps, causal, normalize, act):
+    """Call the library through the registered op (the C ABI), no dispatch logic."""
+    return torch.ops.avey_kernels.contextualize(z, v, gate, bias, valid, float(eps), 1e-12, causal, normalize, act)
+
+
+def _report(out, want):
+    diff = np.abs(out - want)
+    row_err = np.linalg.norm(out - want, axis=-1) / np.maximum(np.linalg.norm(want, axis=-1), 1e-30)
+    return float(diff.max()), float(row_err.max())
+
+
+def _assert_close(out, want, dtype, label='', cond=None):
+    """allclose at the dtype's tolerance; with ``cond`` (per-row Avey-B condition
+    numbers) the tolerance of each row grows with its conditioning, the way a
+    sum that cancels amplifies rounding (the reference relaxes to 3e-4 for the
+    same reason, tests/test_triton.py:243-249)."""
+    out = _np(out)
+    tol = TOL[dtype]
+    # Values beyond the output type's range round to +-inf in the reference's
+    # final cast (ops.py:91); they must overflow the same way here.
+    want_cast = torch.from_numpy(np.asarray(want, dtype=np.float64)).to(dtype).double().numpy()
+    over = ~np.isfinite(want_cast)
+    assert np.array_equal(out[over], want_cast[over]), f'{label} overflow positions differ'
+    assert np.all(np.isfinite(out[~over])), label
+    if over.any():
+        out = np.where(over, 0.0, out)
+        want = np.where(over, 0.0, want)
+    max_abs, row = _report(out, want)
+    if cond is not None:
+        scale = (1.0 + cond)[..., None]
+        bad = np.abs(out - want) > tol * scale * (1.0 + np.abs(want))
+        assert not bad.any(), f'{label} {int(bad.sum())} elements beyond tol*(1+cond); max_abs={max_abs:.3e}'
+        return max_abs, row
+    np.testing.assert_allclose(out, want, rtol=tol, atol=tol, err_msg=f'{label} max_abs={max_abs:.3e} row={row:.3e}')
+    if dtype == torch.bfloat16:
+        assert row <= 1e-2, f'{label} row-normwise error {row:.3e}'
+    return max_abs, row
+
+
+def test_library_is_loaded_and_device_supported():
+    lib = _hip.load()
+    assert lib.avey_abi_version() == 1
+    assert _hip.device_supported(DEV)
+
+
+SHAPES = [(1, 1), (5, 7), (35, 37), (67, 65), (161, 37), (35, 133), (67, 257), (33, 1000), (130, 1100)]
+COMBOS = [(False, True, 'identity'), (False, False, 'silu'), (True, False, 'relu'), (True, False, 'gelu'),
+          (True, False, 'relu2')]
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32, torch.float64],
+                         ids=lambda d: str(d).replace('torch.', ''))
+@pytest.mark.parametrize('c,d', SHAPES)
+def test_tail_shapes_all_flags_nan_padding(dtype, c, d):
+    g = torch.Generator().manual_seed(17 * c + d)
+    z = torch.randn(2, c, d, generator=g)
+    z[:, 0] = 0.0  # an all-zero valid row: the norm clamp path
+    gate = torch.randn(2, c, d, generator=g)
+    bias = torch.randn(d, generator=g)
+    v = torch.randn(c, c, generator=g)
+    valid = torch.ones(2, c, dtype=torch.bool)
+    if c > 1:
+        valid[0, -1] = False
+        valid[1, 1::3] = False
+        z[~valid] = float('nan')
+        gate[~valid] = float('nan')
+    z, gate, bias, v = (t.to(dtype).to(DEV) for t in (z, gate, bias, v))
+    valid = valid.to(DEV)
+    for normalized, causal, act in COMBOS:
+        eps = 0.25 if normalized else 1e-6
+        vv = None if normalized else v
+        out = _fused(z, vv, gate, bias, valid, eps=eps, causal=causal, normalize=normalized, act=act)
+        assert out.dtype == dtype
+        want = _oracle(z, vv, gate, bias, valid, eps=eps, causal=causal, normalize=normalized, act=act)
+        cond = orc.row_condition(_np(z), valid.cpu().numpy(), eps=eps) if normalized else None
+        _assert_close(out, want, dtype, f'c={c} d={d} norm={normalized} causal={causal} act={act}', cond)
+        assert torch.all(out[~valid] == 0)
+        # Without the optional operands as well.
+        out2 = _fused(z.nan_to_num(), vv, None, None, None, eps=eps, causal=causal, normalize=normalized, act=act)
+        want2 = _oracle(z.nan_to_num(), vv, None, None, None, eps=eps, causal=causal, normalize=normalized, act=act)
+        cond2 = orc.row_condition(_np(z.nan_to_num()), eps=eps) if normalized else None
+        _assert_close(out2, want2, dtype, f'bare c={c} d={d} norm={normalized} causal={causal}', cond2)
+
+
+@pytest.mark.parametrize('case', load_kats()['cases'], ids=lambda c: c['name'])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16], ids=['fp32', 'bf16'])
+def test_known_answers_on_gpu(case, dtype):
+    if case['dtype'] == 'float64':
+        dtype = torch.float64
+    z = torch.tensor(case['z_tr'], dtype=dtype, device=DEV)
+    kw = dict(case['kwargs'])
+    for key in ('z_tl', 'bias'):
+        if key in case:
+            kw[key] = torch.tensor(case[key], dtype=dtype, device=DEV)
+    if 'valid' in case:
+        kw['valid'] = torch.tensor(case['valid'], device=DEV)
+    if case['op'] == 'avey':
+        out = avey(z, torch.tensor(case['v'], dtype=dtype, device=DEV), backend='hip', **kw)
+    else:
+        out = avey_b(z, backend='hip', **kw)
+    tol = dict(rtol=case['rtol'], atol=case['atol']) if dtype != torch.bfloat16 else dict(rtol=1e-2, atol=1e-2)
+    exp = case.get('expected')
+    if exp is None:
+        torch.testing.assert_close(out[0, 0].double().cpu(), torch.tensor(case['expected_row0'], dtype=torch.float64),
+                                   **tol)
+    else:
+        torch.testing.assert_close(out.double().cpu(), torch.tensor(exp, dtype=torch.float64), **tol)
+
+
+def _config_case(tag):
+    cfg = wl.CONFIGS[tag]
+    inp = wl.make_inputs(cfg, device=DEV)
+    return cfg, inp
+
+
+@pytest.mark.parametrize('tag', ['C1', 'C2', 'C3', 'C4', 'C5'])
+def test_benchmark_configs_full_size(tag):
+    cfg, inp = _config_case(tag)
+    print(f'\n[{cfg.name}] plan={_hip.plan(inp["z_tr"].shape, cfg.dtype, causal=cfg.causal, normalize=cfg.op == "avey_b")}',
+          flush=True)
+    out = wl.call(cfg, inp)
+    torch.cuda.synchronize()
+    normalize = cfg.op == 'avey_b'
+    acc = np.float64 if tag in ('C1', 'C2', 'C5') else np.float32
+    want = _oracle(inp['z_tr'], None if normalize else inp['v'], inp['z_tl'], inp['bias'], inp['valid'],
+                   eps=1e-6, causal=cfg.causal, normalize=normalize, act='identity', acc=acc)
+    cond = None
+    if normalize:
+        cond = orc.row_condition(_np(inp['z_tr']), None if inp['valid'] is None else inp['valid'].cpu().numpy())
+        print(f'[{cfg.name}] Avey-B row condition: median {np.median(cond):.2f} max {cond.max():.3e} '
+              f'rows>10: {int((cond > 10).sum())}/{cond.size}', flush=True)
+        # Well-conditioned rows must meet the plain bound as well.
+        good = cond < 4
+        _assert_close(out.cpu()[torch.from_numpy(good)], want[good], cfg.dtype, cfg.name + ' cond<4')
+    max_abs, row = _assert_close(out, want, cfg.dtype, cfg.name, cond)
+    print(f'[{cfg.name}] max_abs={max_abs:.3e} row_normwise={row:.3e}', flush=True)
+
+
+@pytest.mark.parametrize('tag', ['C3', 'C5'])
+def test_avey_b_configs_weighted_variant(tag):
+    # The V-weighted, bidirectional avey call on the Avey-B configs' inputs.
+    cfg, inp = _config_case(tag)
+    out = avey(inp['z_tr'], inp['v'], z_tl=inp['z_tl'], bias=inp['bias'], valid=inp['valid'], causal=False,
+               backend='hip')
+    want = _oracle(inp['z_tr'], inp['v'], inp['z_tl'], inp['bias'], inp['valid'], eps=1e-6, causal=False,
+                   normalize=False, act='identity', acc=np.float32)
+    _assert_close(out, want, cfg.dtype, f'{cfg.name} weighted')
+
+
+def test_bitwise_determinism_full_size():
+    for tag in ('C2', 'C4'):
+        cfg, inp = _config_case(tag)
+        a = wl.call(cfg, inp)
+        b = wl.call(cfg, inp)
+        assert torch.equal(a, b), tag
+
+
+def test_causal_rows_blind_to_future_full_size():
+    cfg, inp = _config_case('C4')
+    a = wl.call(cfg, inp)
+    half = cfg.context // 2 + 7
+    inp2 = dict(inp)
+    z2 = inp['z_tr'].clone()
+    z2[:, half:] = torch.randn_like(z2[:, half:])
+    inp2['z_tr'] = z2
+    b = wl.call(cfg, inp2)
+    assert torch.equal(a[:, :half], b[:, :half])
+    assert not torch.equal(a[:, half:], b[:, half:])
+
+
+def test_padded_rows_are_exact_zeros_and_nan_safe_full_size():
+    cfg, inp = _config_case('C5')
+    z = inp['z_tr'].clone()
+    valid = inp['valid']
+    z[~valid] = float('nan')
+    inp2 = dict(inp, z_tr=z)
+    out = wl.call(cfg, inp2)
+    ref = wl.call(cfg, inp)
+    assert torch.all(out[~valid] == 0)
+    assert torch.equal(out, ref)
+
+
+def test_activations_and_fp16_at_headline_shape():
+    cfg, inp = _config_case('C2')
+    for dtype in (torch.bfloat16, torch.float16):
+        z, gate, v, bias = (inp[k].to(dtype) for k in ('z_tr', 'z_tl', 'v', 'bias'))
+        bias = torch.randn_like(bias) * 0.1
+        for act in ('silu', 'gelu', 'relu2'):
+            out = avey(z, v, z_tl=gate, bias=bias, activation=act, backend='hip')
+            want = _oracle(z, v, gate, bias, None, eps=1e-6, causal=True, normalize=False, act=act, acc=np.float32)
+            _assert_close(out, want, dtype, f'C2 {dtype} {act}')
+
+
+def test_noncontiguous_inputs_match_contiguous():
+    g = torch.Generator().manual_seed(3)
+    base = torch.randn(2, 70, 35, generator=g).to(DEV, torch.bfloat16)
+    z = base.transpose(1, 2)  # [2, 35, 70] view
+    out = avey_b(z, backend='hip')
+    ref = avey_b(z.contiguous(), backend='hip')
+    assert torch.equal(out, ref)
+
+
+def test_gradient_request_falls_back_and_hip_backend_refuses():
+    z = torch.rand(2, 35, 37, device=DEV, requires_grad=True)
+    out = avey_b(z)
+    out.sum().backward()
+    assert z.grad is not None and torch.isfinite(z.grad).all()
+    with pytest.raises(ValueError):
+        avey_b(z, backend='hip')
+
+
+def test_hip_graph_replay_matches_eager():
+    cfg, inp = _config_case('C2')
+    eager = wl.call(cfg, inp).clone()
+    static_in = {k: (t.clone() if t is not None else None) for k, t in inp.items()}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            wl.call(cfg, static_in)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = wl.call(cfg, static_in)
+    for i in range(4):
+        static_in['z_tr'].copy_(inp['z_tr'])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), f'replay {i}'
+        # Eager work between replays.
+        _ = wl.call(cfg, inp)
+        torch.cuda.synchronize()
