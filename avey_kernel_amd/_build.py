@@ -17,10 +17,12 @@ CSRC = os.path.join(PKG_DIR, 'csrc')
 INCLUDE = os.path.join(REPO_DIR, 'include')
 BUILD_DIR = os.path.join(PKG_DIR, '_build')
 LIB_PATH = os.path.join(PKG_DIR, 'libavey_hip.so')
-SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip')
+SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip', 'avey_fused_bm16.hip',
+           'avey_fused_bm32.hip', 'avey_fused_bm64.hip')
 ARCH = 'gfx950'
 
-# -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (see the design notes).
+# -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32; some of their
+# forms have given wrong results on MI355X without any error.
 HIP_FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
              '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
              '-Wno-pass-failed', '-I', INCLUDE, '-I', CSRC]

@@ -78,13 +78,16 @@ bool device_ok(int dev) {
 // The static tile table (replaces the reference's runtime autotuner,
 // avey_kernels/_triton.py:131-150). For the fused kernel:
 //   * slice width DS = 32 * ceil(D / 128) features per wave (4 waves cover D);
-//   * BM = 64 query rows when the wave's accumulators fit (DS <= 192), else 32;
+//   * BM = 64 query rows while the wave's registers hold the query fragments,
+//     accumulators and a key tile without spilling (DS <= 192), else 32;
 //   * BM halves (down to 16) while the grid would leave CUs of the 256 idle.
 Plan make_plan(const avey_fwd_args& a) {
   Plan pl{};
   const bool low = a.dtype == AVEY_DTYPE_BF16 || a.dtype == AVEY_DTYPE_F16;
   const int nk = slice_steps(a.features);
-  if (low && nk > 0) {
+  // The fused kernel indexes within one batch item with 32-bit offsets.
+  const bool small_item = a.context * a.features < (int64_t(1) << 31) && a.batch < (int64_t(1) << 31);
+  if (low && nk > 0 && small_item) {
     pl.kernel = 1;
     pl.bn = 32;
     pl.bd = 32 * nk;

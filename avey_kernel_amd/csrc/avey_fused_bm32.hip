@@ -1,0 +1,13 @@
+// Fused kernel variants with 32 query rows per workgroup (bf16 and fp16).
+#include "avey_fused.h"
+
+namespace avey {
+
+template <>
+hipError_t launch_fused_bm<32>(const FwdParams& p, int dtype, int nk, int64_t grid, hipStream_t s) {
+  if (dtype == AVEY_DTYPE_BF16) return launch_fused_nk<__bf16, 32>(p, nk, grid, s);
+  if (dtype == AVEY_DTYPE_F16) return launch_fused_nk<_Float16, 32>(p, nk, grid, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace avey

@@ -97,7 +97,7 @@ def test_static_tile_table():
     # Causal skipping visits about half the key tiles of the full traversal.
     full = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=False, normalize=False)
     half = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=True, normalize=False)
-    assert half['block_m'] == full['block_m']
+    assert half["block_m"] == full["block_m"]
     assert abs(half['key_tile_steps'] / full['key_tile_steps'] - 0.5) < 0.02
     # fp32 / fp64 and very wide features take the generic kernel, which needs a workspace.
     for dt in (torch.float32, torch.float64):
