@@ -41,10 +41,17 @@ def parse_args():
     ap.add_argument('--config', default='C2')
     ap.add_argument('--cpu-seconds', type=float, default=10.0)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    ap.add_argument('--cold-calls', type=int, default=30)
+    ap.add_argument('--cold-calls', type=int, default=0,
+                    help='also time this many calls with the MALL flushed before each (off by default so that '
+                         'every traced dispatch of the default run is a warm one)')
     ap.add_argument('--all-configs', action='store_true',
                     help='also measure every configuration (table on stderr, --report JSON)')
     ap.add_argument('--report', default=None, help='write all measurements to this JSON file')
+    ap.add_argument('--dispatches', type=int, default=0,
+                    help='profiling run: launch the config this many times (eager, no timing, no JSON) '
+                         'after one plain copy of --copy-mib MiB, whose HBM counters calibrate the '
+                         'per-dispatch FETCH_SIZE / WRITE_SIZE readings')
+    ap.add_argument('--copy-mib', type=int, default=256)
     return ap.parse_args()
 
 
@@ -170,15 +177,36 @@ def roofline_block(flops, nbytes, per_call_ms, traffic):
 
 
 def load_traffic(tag):
-    """HBM bytes per dispatch from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', f'fused_fwd_{tag}_hbm_traffic.txt')
-    if not os.path.exists(path):
-        return None
-    with open(path) as fh:
-        for line in fh:
-            if line.startswith('traffic_bytes_per_dispatch:'):
-                return int(float(line.split(':', 1)[1]))
+    """HBM bytes per dispatch from the committed rocprofv3 PMC summary for this config, if present.
+
+    profiles/<kernel>_<tag>_hbm_traffic.txt holds FETCH_SIZE + WRITE_SIZE per dispatch, each scaled
+    by what the same counter reads for a plain copy of known size.
+    """
+    import glob
+    root = os.path.dirname(os.path.abspath(__file__))
+    for path in sorted(glob.glob(os.path.join(root, 'profiles', f'*_{tag}_hbm_traffic.txt'))):
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith('traffic_bytes_per_dispatch:'):
+                    return int(float(line.split(':', 1)[1]))
     return None
+
+
+def profile_dispatches(torch, wl, tag, n, copy_mib):
+    """Launch sequence for rocprofv3 counter runs: one copy of known size, then n calls."""
+    src = torch.empty(copy_mib << 20, dtype=torch.uint8, device='cuda').fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)  # reads and writes exactly copy_mib MiB each
+    torch.cuda.synchronize()
+    del src, dst
+    cfg = wl.CONFIGS[tag]
+    inp = wl.make_inputs(cfg, device='cuda')
+    for _ in range(n):
+        wl.call(cfg, inp, backend='hip')
+    torch.cuda.synchronize()
+    log(f'[bench] profiled {n} dispatches of {cfg.name} after a {copy_mib} MiB copy; '
+        f'compulsory bytes {wl.compulsory_bytes(cfg)}')
 
 
 def main():
@@ -199,6 +227,9 @@ def main():
     torch.cuda.set_device(0)
     props = torch.cuda.get_device_properties(0)
     log(f'[bench] device {props.name} {getattr(props, "gcnArchName", "")} CUs {props.multi_processor_count}')
+    if args.dispatches > 0:
+        profile_dispatches(torch, wl, args.config, args.dispatches, args.copy_mib)
+        return
 
     cfg, inp, flops, nbytes, per_call_ms, wall_ms, eager_ms, cold_ms = measure_config(
         torch, wl, args.config, args.steps, args.warmup, args.cold_calls)
