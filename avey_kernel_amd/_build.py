@@ -17,8 +17,8 @@ CSRC = os.path.join(PKG_DIR, 'csrc')
 INCLUDE = os.path.join(REPO_DIR, 'include')
 BUILD_DIR = os.path.join(PKG_DIR, '_build')
 LIB_PATH = os.path.join(PKG_DIR, 'libavey_hip.so')
-SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip', 'avey_fused_bm16.hip',
-           'avey_fused_bm32.hip', 'avey_fused_bm64.hip')
+SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip') + tuple(
+    f'avey_fused_bm{bm}_{t}.hip' for bm in (64, 32, 16) for t in ('bf16', 'f16'))
 ARCH = 'gfx950'
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32; some of their

@@ -78,16 +78,22 @@ bool device_ok(int dev) {
 // The static tile table (replaces the reference's runtime autotuner,
 // avey_kernels/_triton.py:131-150). For the fused kernel:
 //   * slice width DS = 32 * ceil(D / 128) features per wave (4 waves cover D);
-//   * BM = 64 query rows while the wave's registers hold the query fragments,
-//     accumulators and a key tile without spilling (DS <= 192), else 32;
+//   * BM = 64 query rows while the double-buffered key slices and the partial
+//     similarity tiles fit the 160 KB of LDS (DS <= 192), else 32;
 //   * BM halves (down to 16) while the grid would leave CUs of the 256 idle.
+// The fused kernel addresses memory with 16-byte row chunks and 32-bit buffer
+// offsets, so it also needs D % 8 == 0, 16-byte aligned z_tr / z_tl / out, an
+// 8-byte aligned bias, at most 2^30 elements per batch item and C <= 32768 (V
+// under 2 GiB); other shapes take the generic kernel.
 Plan make_plan(const avey_fwd_args& a) {
   Plan pl{};
   const bool low = a.dtype == AVEY_DTYPE_BF16 || a.dtype == AVEY_DTYPE_F16;
   const int nk = slice_steps(a.features);
-  // The fused kernel indexes within one batch item with 32-bit offsets.
-  const bool small_item = a.context * a.features < (int64_t(1) << 31) && a.batch < (int64_t(1) << 31);
-  if (low && nk > 0 && small_item) {
+  const auto al = [](const void* x, uintptr_t n) { return x == nullptr || ((uintptr_t)x & (n - 1)) == 0; };
+  const bool layout = a.features % 8 == 0 && al(a.z_tr, 16) && al(a.z_tl, 16) && al(a.out, 16) && al(a.bias, 8);
+  const bool small_item = a.context * a.features < (int64_t(1) << 30) && a.context <= 32768 &&
+                          a.batch < (int64_t(1) << 31);
+  if (low && nk > 0 && layout && small_item) {
     pl.kernel = 1;
     pl.bn = 32;
     pl.bd = 32 * nk;
@@ -198,8 +204,6 @@ int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, vo
   p.act = a->activation;
   p.eps = a->eps;
   p.norm_eps = a->norm_eps;
-  const auto al16 = [](const void* x) { return x == nullptr || ((uintptr_t)x & 15) == 0; };
-  p.aligned = (a->features % 8 == 0) && al16(a->z_tr) && al16(a->z_tl) && al16(a->out);
 
   hipStream_t s = (hipStream_t)stream;
   e = pl.kernel == 1 ? launch_fused(p, a->dtype, pl, s) : launch_generic(p, a->dtype, pl, s);

@@ -19,7 +19,6 @@ struct FwdParams {
   void* work;           // scratch (generic path: per-row inverse norms)
   int64_t B, C, D;
   int32_t causal, normalize, act;
-  int32_t aligned;      // D % 8 == 0 and z/gate/out 16-byte aligned, bias 8-byte aligned
   double eps, norm_eps;
 };
 
