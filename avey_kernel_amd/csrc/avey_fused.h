@@ -105,6 +105,16 @@ __device__ __forceinline__ void st64(u32x2 v, rsrc_t r, uint32_t off) {
 
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+template <int I>
+using IC = std::integral_constant<int, I>;
+
+// Hides a value from the optimizer, so that a select feeding a load's offset stays
+// a select instead of becoming a branch around two loads.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 template <typename T16> struct Ops;
 template <> struct Ops<__bf16> {
   // Bits of 1.0 in the type's 16-bit storage, shifted to where to_f expects them.
@@ -177,32 +187,92 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// LDS-geometry of one (BM, NK) variant. Key tiles, the query rows and the gate
+// rows live in LDS as per-wave "slices": wave w's 32 * NK features of a row,
+// stored as CPRP 16-byte chunks (CPR real ones, padded to whole 128-byte groups).
+// Chunk c of row r sits at position r * CPRP + swizzle(r, c), an XOR of c's low
+// bits with a permutation of r's low bits, within groups of G chunks. With it the
+// similarity operand reads (16 rows, one chunk), the transposed mixing reads (4
+// rows, two chunks) and the epilogue reads all hit distinct LDS banks, while every
+// 128-byte group still arrives from one 128-byte run of global memory.
 template <int BM, int NK>
-struct Smem {
-  static constexpr int QB = BM / 16;
-  static constexpr int ZLD = 32 * NK + 8;  // row stride in elements; +16 B staggers LDS banks
-  uint16_t zs[2][kWaves][kBN][ZLD];        // each wave's slice of a key tile, two tiles
-  f32x4 sx[kWaves][2][QB][64];  // per-wave partial S^T tiles (key half, query block)
-  u32x4 px[QB][64];             // P as mixing-product B operands (8 x 16-bit per lane)
-  float nxp[kWaves][kBN];       // per-wave partial sums of squares of the keys; -1: padded key
-  float rk[kBN];                // 1 / max(||k||, norm_eps); 0 for padded or out-of-range keys
-  float nq[kWaves][BM];         // per-wave partial sums of squares of the queries
-  float rq[BM];                 // 1 / max(||q||, norm_eps); 0 for padded or out-of-range rows
-  float dx[QB][2][4][16];       // signed row-sum partials
-  float dq[BM];                 // full signed row sums
+struct Geo {
+  static constexpr int QB = BM / 16, DS = 32 * NK, NT = DS / 16;
+  static constexpr int CPR = 4 * NK;
+  static constexpr int CPRP = (CPR + 7) / 8 * 8;
+  static constexpr int G = CPRP % 16 == 0 ? 16 : 8;
+  static constexpr int SLICE = kBN * CPRP * 16;  // bytes of one wave's rows of a key tile
+  static constexpr int TILE = kWaves * SLICE;    // bytes of one ring slot
+  static constexpr int KDMA = kBN * CPRP / 64;   // DMA instructions per wave per key tile
+  // Lane offsets of consecutive DMA instructions repeat every P instructions, which
+  // cover RPP = 16 rows (the swizzle's period): only P offsets are kept, and the
+  // rows they advance go into the resource base.
+  static constexpr int P = CPRP / 4;
+  static constexpr int RPP = 16;
+  static constexpr int SX = kWaves * 2 * QB * 64 * 16;
+  static constexpr int PX = (QB + 1) * 64 * 16;
+  // The query rows of the prologue take ring slot R-1 and, for BM = 64, this
+  // region too, which later holds the partial similarities and P.
+  static constexpr int OVF = (BM > 32 && TILE > SX + PX) ? TILE : SX + PX;
+  static constexpr int SMALL = 4 * (kWaves * kBN + kBN + kWaves * BM + BM + (QB + 1) * 2 * 4 * 16 + BM);
+  static constexpr int kLdsMax = 160 * 1024;
+  // Ring depth: three slots when they fit, else two.
+  static constexpr int R = (3 * TILE + OVF + SMALL <= kLdsMax) ? 3 : 2;
+  static_assert(2 * TILE + OVF + SMALL <= kLdsMax, "tile does not fit the LDS");
+  static_assert(BM <= 32 * R, "query rows must fit the ring");
 };
+
+template <int G>
+__device__ __forceinline__ int swz(int r) {
+  const int h = G == 8 ? (r & 15) >> 1 : (r & 15);
+  return G == 8 ? (((h << 1) & 7) | (h >> 2)) : (((h << 1) & 15) | (h >> 3));
+}
+template <int G>
+__device__ __forceinline__ int swzc(int r, int c) {
+  return (c & ~(G - 1)) | ((c ^ swz<G>(r)) & (G - 1));
+}
+
+template <int BM>
+struct SmallLds {
+  float nxp[kWaves][kBN];            // per-wave partial sums of squares of the keys; -1: padded key
+  float rk[kBN];                     // 1 / max(||k||, norm_eps); 0 for padded or out-of-range keys
+  float nq[kWaves][BM];              // per-wave partial sums of squares of the queries
+  float rq[BM];                      // 1 / max(||q||, norm_eps); 0 for padded or out-of-range rows
+  float dx[BM / 16 + 1][2][4][16];   // signed row-sum partials; last row: sink of idle waves
+  float dq[BM];                      // 1 / (full signed row sum + eps)
+};
+
+// Global -> LDS copy of 16 bytes per lane: lane l's bytes land at lds + 16 l.
+__device__ __forceinline__ void dma16(rsrc_t r, char* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
+__device__ __forceinline__ void st128(u32x4 v, rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+// s_waitcnt lgkmcnt(0), leaving the vector-memory counters alone: the wave's LDS
+// reads of a ring slot have finished before a DMA refills it.
+__device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 }  // namespace
 
-// FULL: D == 4 * 32 * NK, so every 16-byte chunk a wave touches lies inside the
-// row. Otherwise chunks at or past D are redirected to kNowhere (D % 8 == 0 makes
-// a chunk wholly in or out).
+// FULL: D == 4 * 32 * NK, so every chunk a wave touches lies inside the row.
+// Otherwise chunks at or past D are redirected to kNowhere (D % 8 == 0 makes a
+// chunk wholly in or out).
 template <typename T16, int BM, int NK, bool FULL>
 __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
-  typedef Smem<BM, NK> S;
-  constexpr int QB = S::QB, DS = 32 * NK, NT = DS / 16;
+  typedef Geo<BM, NK> Gm;
+  constexpr int QB = Gm::QB, DS = Gm::DS, NT = Gm::NT, CPR = Gm::CPR, CPRP = Gm::CPRP, G = Gm::G;
+  constexpr int SLICE = Gm::SLICE, TILE = Gm::TILE, R = Gm::R, KDMA = Gm::KDMA;
   constexpr int UNITS = 2 * QB, UPW = (UNITS + kWaves - 1) / kWaves;
-  __shared__ S sm;
+  // One LDS object per ring slot: the compiler's wait for a slot's DMA then covers
+  // that slot only, not the refills in flight for the others.
+  __shared__ __attribute__((aligned(16))) char slot0[TILE];
+  __shared__ __attribute__((aligned(16))) char slot1[TILE];
+  __shared__ __attribute__((aligned(16))) char slot2[R == 3 ? TILE : 16];
+  __shared__ __attribute__((aligned(16))) char ovf[Gm::OVF];
+  __shared__ SmallLds<BM> sm;
+  f32x4(*const sx)[2][QB][64] = reinterpret_cast<f32x4(*)[2][QB][64]>(ovf);           // [wave][kb][qb][lane]
+  u32x4(*const px)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX);                // [qb (QB: sink)][lane]
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
@@ -226,51 +296,91 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   const float norm_eps = (float)p.norm_eps;
   const float eps2 = norm_eps * norm_eps;
   const float inv_eps = 1.f / norm_eps;
+  const int nkt = (int)key_tiles_for(qt, C, BM, kBN, causal);
 
-  // Byte offsets of this lane's 16-byte chunks within a 16-row block: row li,
-  // features fw + 32 s + 8 lg .. +7.
-  uint32_t coff[NK];
+  // ---- addressing -------------------------------------------------------------------
+  // This wave's part of ring slot I, and row group j (32 rows) of the query region
+  // (prologue) and of the gate / output region (epilogue).
+  auto slot_base = [&](auto slot) -> char* {
+    constexpr int I = decltype(slot)::value;
+    char* s = I == 0 ? slot0 : (I == 1 ? slot1 : slot2);
+    return s + w * SLICE;
+  };
+  auto qrows_base = [&](int j) -> char* { return j == 0 ? ((R == 3 ? slot2 : slot1) + w * SLICE) : (ovf + w * SLICE); };
+  auto erows_base = [&](int j) -> char* { return (j == 0 ? slot0 : slot1) + w * SLICE; };
+
+  // Global byte offset (from a region's first row) of slice position pos, i.e. row
+  // pos / CPRP, chunk swizzle(row, pos % CPRP); kNowhere past the slice or past D.
+  auto goff = [&](int pos) -> uint32_t {
+    const int r = pos / CPRP, c = swzc<G>(r, pos % CPRP);
+    const int col = fw + 8 * c;
+    return (c < CPR && (FULL || col < D)) ? (uint32_t)r * row_bytes + (uint32_t)col * 2u : kNowhere;
+  };
+  constexpr int P = Gm::P, RPP = Gm::RPP;
+  uint32_t kof[P];
 #pragma unroll
-  for (int s = 0; s < NK; ++s) {
-    const int col = fw + 32 * s + 8 * lg;
-    coff[s] = (FULL || col < D) ? (uint32_t)li * row_bytes + (uint32_t)col * 2u : kNowhere;
+  for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
+  // LDS byte offsets of this lane's fragments inside a slice (see Geo):
+  //   a1: similarity operands, row li, chunk 4 s + lg          (s % (G / 4) picks the entry)
+  //   a2: transposed mixing operands, row 4 lg + li / 4, chunk 2 t + (li & 3) / 2, half li & 1
+  //   a3: epilogue, row li, chunk 2 t + lg / 2, half lg & 1     (t % (G / 2) picks the entry)
+  uint32_t a1[G / 4], a2[G / 2];
+#pragma unroll
+  for (int m = 0; m < G / 4; ++m) a1[m] = 16u * (uint32_t)(li * CPRP + swzc<G>(li, 4 * m + lg));
+  {
+    const int r0 = 4 * lg + (li >> 2);
+#pragma unroll
+    for (int m = 0; m < G / 2; ++m)
+      a2[m] = 16u * (uint32_t)(r0 * CPRP + swzc<G>(r0, 2 * m + ((li & 3) >> 1))) + 8u * (uint32_t)(li & 1);
   }
-  auto chunk_off = [&](int s) -> uint32_t {
-    if constexpr (FULL) return coff[0] + 64u * (uint32_t)s;  // folds into the instruction offset
-    else return coff[s];
+  auto frag_a = [&](const char* base, int row16, int s) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(base + a1[s % (G / 4)] + 16 * (16 * row16 * CPRP + G * (s / (G / 4))));
   };
 
-  // Reduction units owned by this wave: unit u = w + 4j -> (query block u/2, key half u%2).
-  int uq[UPW], uk[UPW], ud[UPW];
+  // Reduction units: unit u = w + 4j -> (query block u/2, key half u%2). Waves
+  // with fewer real units than UPW run a copy of unit 0 whose results go to the
+  // sink rows, so every wave executes the same branch-free code.
+  int uq[UPW], uk[UPW], pq[UPW];
+  float ud[UPW];
   uint32_t voff[UPW];
 #pragma unroll
   for (int j = 0; j < UPW; ++j) {
-    const int u = (w + kWaves * j) < UNITS ? w + kWaves * j : 0;
+    const bool real = (UNITS % kWaves == 0) || (w + kWaves * j < UNITS);
+    const int u = real ? w + kWaves * j : 0;
     uq[j] = u >> 1;
     uk[j] = u & 1;
+    pq[j] = real ? uq[j] : QB;
     // key - query = ud + i - (q0 - k0) for the lane's keys i = 0..3
-    ud[j] = 16 * uk[j] + 4 * lg - 16 * uq[j] - li;
+    ud[j] = (float)(16 * uk[j] + 4 * lg - 16 * uq[j] - li);
     // V[q][k0 + 16 uk + 4 lg + i] relative to V + k0: row q = q0 + 16 uq + li
     voff[j] = ((uint32_t)(q0 + 16 * uq[j] + li) * (uint32_t)C + (uint32_t)(16 * uk[j] + 4 * lg)) * 2u;
   }
   const uint32_t vbytes = has_v ? (uint32_t)C * (uint32_t)C * 2u : 0u;
 
-  // ---- loads of one key tile (similarity A operands and validity) -----------------
-  u32x4 zf[2][NK];
-  uint32_t zv[2];
-  auto load_keys = [&](int k0) {
+  // ---- loads ------------------------------------------------------------------------
+  // Key tile t (its 32 rows, this wave's slice) into ring slot I, with the validity
+  // bytes of its two 16-row blocks (rows past the context read 0 and are told apart
+  // by their index). Tiles past the last are not fetched.
+  uint32_t zv[R][2];
+  auto fetch_keys = [&](int t, auto slot) {
+    constexpr int I = decltype(slot)::value;
+    if (t >= nkt) return;
+    const int k0 = t * kBN;
+    char* base = slot_base(slot);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const rsrc_t rz = rows_rsrc(zb, k0 + 16 * kb, C, row_bytes);
-      const rsrc_t rv = rows_rsrc(vb, k0 + 16 * kb, valid_rows, 1u);
-      zv[kb] = ld8(rv, (uint32_t)li);
+    for (int j = 0; j < KDMA; ++j) dma16(rows_rsrc(zb, k0 + RPP * (j / P), C, row_bytes), base + 1024 * j, kof[j % P]);
 #pragma unroll
-      for (int s = 0; s < NK; ++s) zf[kb][s] = ld128(rz, chunk_off(s));
-    }
+    for (int kb = 0; kb < 2; ++kb) zv[I][kb] = ld8(rows_rsrc(vb, k0 + 16 * kb, valid_rows, 1u), (uint32_t)li);
+  };
+  // BM rows of a [B][C][D] tensor from row q0 into a row region (prologue: the
+  // queries; epilogue: the gate).
+  auto fetch_rows = [&](const char* src, auto region) {
+#pragma unroll
+    for (int j = 0; j < BM * CPRP / 64; ++j)
+      dma16(rows_rsrc(src, q0 + RPP * (j / P), C, row_bytes), region(j / KDMA) + 1024 * (j % KDMA), kof[j % P]);
   };
   // V entries of tile k0 for this wave's units (raw 16-bit words).
-  uint32_t vv[UPW][4];
-  auto load_v = [&](int k0) {
+  auto load_v = [&](int k0, uint32_t (&vv)[UPW][4]) {
     const uint32_t skip = (uint32_t)k0 * 2u;
     const rsrc_t r = make_rsrc((const char*)(has_v ? p.v : p.z) + skip, vbytes > skip ? vbytes - skip : 0u);
 #pragma unroll
@@ -279,33 +389,26 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
       for (int i = 0; i < 4; ++i) vv[j][i] = ld16(r, voff[j] + 2u * (uint32_t)i);
   };
 
-  const int nkt = (int)key_tiles_for(qt, C, BM, kBN, causal);
-  load_keys(0);
-
-  // ---- prologue: query rows as similarity B operands, and their norms ------------
+  // ---- prologue: the first R-1 key tiles, the query rows and their norms ------------
+  fetch_keys(0, IC<0>{});
+  if constexpr (R == 3) fetch_keys(1, IC<1>{});
+  fetch_rows((const char*)zb, qrows_base);
+  uint32_t qv[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
   u32x4 qf[QB][NK];
-  {
-    uint32_t qv[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const rsrc_t rz = rows_rsrc(zb, q0 + 16 * qb, C, row_bytes);
-      const rsrc_t rv = rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u);
-      qv[qb] = ld8(rv, (uint32_t)li);
+  for (int qb = 0; qb < QB; ++qb) {
+    const bool ok = (16 * qb + li < C - q0) && ((qv[qb] | or_valid) != 0u);
+    float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < NK; ++s) qf[qb][s] = ld128(rz, chunk_off(s));
+    for (int s = 0; s < NK; ++s) {
+      const u32x4 x = frag_a(qrows_base(qb >> 1), qb & 1, s);
+      qf[qb][s] = ok ? x : zero4();  // select, so NaN in padded rows never enters
+      ss = Ops<T16>::sumsq(qf[qb][s], ss);
     }
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const bool ok = (16 * qb + li < C - q0) && ((qv[qb] | or_valid) != 0u);
-      float ss = 0.f;
-#pragma unroll
-      for (int s = 0; s < NK; ++s) {
-        qf[qb][s] = ok ? qf[qb][s] : zero4();  // select, so NaN in padded rows never enters
-        ss = Ops<T16>::sumsq(qf[qb][s], ss);
-      }
-      ss = sum_over_groups(ss);
-      if (lg == 0) sm.nq[w][16 * qb + li] = ok ? ss : -1.f;
-    }
+    ss = sum_over_groups(ss);
+    if (lg == 0) sm.nq[w][16 * qb + li] = ok ? ss : -1.f;
   }
 
   f32x4 oacc[NT][QB];
@@ -317,95 +420,99 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
   for (int j = 0; j < UPW; ++j) den[j] = 0.f;
   f32x4 sacc[2][QB];
-  float nkey[2];
+  uint32_t vv[UPW][4];
+  u32x4 ztr[NT];  // transposed mixing operands of the previous tile
 
-  // ---- A(t): partial similarity, key partial norms, staging; next loads ---------------
-  auto stage_a = [&](int t) {
+  // ---- T(t): the mixing operands of tile t, read transposed from its slot -------------
+  auto stage_t = [&](auto slot) {
+    const char* base = slot_base(slot);
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2) {
+      const uint32_t o = a2[t2 % (G / 2)] + 16u * (uint32_t)(G * (t2 / (G / 2)));
+      const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr((const uint16_t*)(base + o)));
+      const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr((const uint16_t*)(base + o + 16 * 16 * CPRP)));
+      ztr[t2] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+
+  // ---- A(t): partial similarity from slot I, key partial norms ------------------------
+  auto stage_a = [&](int t, auto slot) {
+    constexpr int I = decltype(slot)::value;
     const int k0 = t * kBN;
-    uint16_t(*zs)[S::ZLD] = sm.zs[t & 1][w];
-    bool bad = false;
+    char* base = slot_base(slot);
+    if (has_valid) {
+      // Padded rows may hold NaN: once the tile has landed, zero them in this wave's
+      // slice before they reach the products, the norms or the mixing operands.
+      const uint64_t bad0 = __builtin_amdgcn_ballot_w64(lg == 0 && zv[I][0] == 0u);
+      const uint64_t bad1 = __builtin_amdgcn_ballot_w64(lg == 0 && zv[I][1] == 0u);
+      uint32_t bad = ((uint32_t)bad0 & 0xffffu) | (((uint32_t)bad1 & 0xffffu) << 16);
+      if (bad != 0u) {
+        __builtin_amdgcn_s_waitcnt(0);
+        while (bad != 0u) {
+          const int r = __builtin_ctz(bad);
+          bad &= bad - 1u;
+          if (lane < CPRP) *reinterpret_cast<u32x4*>(base + 16 * (r * CPRP + lane)) = zero4();
+        }
+      }
+    }
+    float nkey[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bool ok = (16 * kb + li < C - k0) && ((zv[kb] | or_valid) != 0u);
+      const bool ok = (16 * kb + li < C - k0) && ((zv[I][kb] | or_valid) != 0u);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < NK; ++s) {
-        // Padded keys may hold NaN: their S^T rows are masked in B and their staged
-        // rows are overwritten with zeros below; the norm slot gets a sentinel.
+        const u32x4 a = frag_a(base, kb, s);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(zf[kb][s], qf[qb][s], sacc[kb][qb]);
-        ss = Ops<T16>::sumsq(zf[kb][s], ss);
-        *reinterpret_cast<u32x4*>(&zs[16 * kb + li][32 * s + 8 * lg]) = zf[kb][s];
+        for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
+        ss = Ops<T16>::sumsq(a, ss);
       }
       ss = sum_over_groups(ss);
       nkey[kb] = ok ? ss : -1.f;
-      bad |= !ok;
     }
-    if (lg == 0) {
-      sm.nxp[w][li] = nkey[0];
-      sm.nxp[w][16 + li] = nkey[1];
-    }
-    // Zero the staged rows of padded / out-of-range keys (tiles at the context's
-    // end, or with key padding) so the mixing product never sees NaN.
-    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bool ok = (16 * kb + li < C - k0) && ((zv[kb] | or_valid) != 0u);
-        if (!ok) {
-#pragma unroll
-          for (int s = 0; s < NK; ++s) *reinterpret_cast<u32x4*>(&zs[16 * kb + li][32 * s + 8 * lg]) = zero4();
-        }
-      }
-    }
-    load_v(k0);
-    load_keys(k0 + kBN < nkt * kBN ? k0 + kBN : C);  // past the last tile: empty resources
+    // Lane groups 0 / 1 write the two key halves (groups 2 / 3 repeat them).
+    sm.nxp[w][16 * (lg & 1) + li] = (lg & 1) ? nkey[1] : nkey[0];
   };
 
-  // ---- B(t): reduce partials, scale, weight, mask, publish P ---------------------------
+  // ---- B(t): reduce partials, scale, weight, mask, publish P; then V of tile t+1 ------
   auto stage_b = [&](int t) {
     const int k0 = t * kBN;
-    const int lim = causal ? q0 - k0 : (1 << 30);
+    // causal: keep key <= query, i.e. ud + i <= q0 - k0
+    const float lim = causal ? (float)(q0 - k0) : 1e30f;
 #pragma unroll
     for (int j = 0; j < UPW; ++j) {
-      if (UNITS % kWaves == 0 || w + kWaves * j < UNITS) {
-        const int qb = uq[j], kb = uk[j];
-        f32x4 sv = sm.sx[0][kb][qb][lane];
+      const int qb = uq[j], kb = uk[j];
+      f32x4 sv = sx[0][kb][qb][lane];
 #pragma unroll
-        for (int x = 1; x < kWaves; ++x) sv += sm.sx[x][kb][qb][lane];
-        const f32x4 rk4 = *reinterpret_cast<const f32x4*>(&sm.rk[16 * kb + 4 * lg]);
-        const float rqv = sm.rq[16 * qb + li];  // 0 for padded / out-of-range queries
-        float pv[4];
+      for (int x = 1; x < kWaves; ++x) sv += sx[x][kb][qb][lane];
+      const f32x4 rk4 = *reinterpret_cast<const f32x4*>(&sm.rk[16 * kb + 4 * lg]);
+      const float rqv = sm.rq[16 * qb + li];  // 0 for padded / out-of-range queries
+      float pv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = sv[i] * (rk4[i] * rqv);
-          x *= Ops<T16>::to_f_or(vv[j][i], or_v);
-          const bool ok = rk4[i] > 0.f && ud[j] + i <= lim;
-          pv[i] = ok ? x : 0.f;
-          den[j] += pv[i];
-        }
-        reinterpret_cast<u32x2*>(&sm.px[qb][lane])[kb] = u32x2{pack2<T16>(pv[0], pv[1]), pack2<T16>(pv[2], pv[3])};
+      for (int i = 0; i < 4; ++i) {
+        // Causal and key-padding masks (padded / out-of-range keys have rk == 0) as
+        // bitwise selects: whatever V holds there, the entry is an exact +0.
+        const uint32_t keep = ((ud[j] + (float)i <= lim) & (rk4[i] > 0.f)) ? 0xffffffffu : 0u;
+        const float x = sv[i] * (rk4[i] * rqv) * Ops<T16>::to_f_or(vv[j][i], or_v);
+        pv[i] = __uint_as_float(__float_as_uint(x) & keep);
+        den[j] += pv[i];
       }
+      reinterpret_cast<u32x2*>(&px[pq[j]][lane])[kb] = u32x2{pack2<T16>(pv[0], pv[1]), pack2<T16>(pv[2], pv[3])};
     }
+    load_v(t + 1 < nkt ? (t + 1) * kBN : C, vv);
   };
 
-  // ---- C(t): mixing; the key rows come back from the wave's LDS slice transposed ---------
-  auto stage_c = [&](int t) {
-    uint16_t(*zs)[S::ZLD] = sm.zs[t & 1][w];
+  // ---- C: mixing of the previous tile from the transposed operands in registers ---------
+  auto stage_c = [&]() {
     u32x4 pf[QB];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) pf[qb] = sm.px[qb][lane];
-    const int row = 4 * lg + (li >> 2);
-    const int colo = 4 * (li & 3);
+    for (int qb = 0; qb < QB; ++qb) pf[qb] = px[qb][lane];
 #pragma unroll
-    for (int t2 = 0; t2 < NT; ++t2) {
-      const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr(&zs[row][16 * t2 + colo]));
-      const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr(&zs[16 + row][16 * t2 + colo]));
-      const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    for (int t2 = 0; t2 < NT; ++t2)
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) oacc[t2][qb] = Ops<T16>::mfma32(a, pf[qb], oacc[t2][qb]);
-    }
+      for (int qb = 0; qb < QB; ++qb) oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pf[qb], oacc[t2][qb]);
   };
 
   // ---- interval-2 publication: A(t)'s partial S^T and the tile's key norms ---------------
@@ -413,15 +520,22 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sm.sx[w][kb][qb][lane] = sacc[kb][qb];
-    if (w == kWaves - 1 && lane < kBN) {
-      const float n = (sm.nxp[0][lane] + sm.nxp[1][lane]) + (sm.nxp[2][lane] + sm.nxp[3][lane]);
-      sm.rk[lane] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
+      for (int qb = 0; qb < QB; ++qb) sx[w][kb][qb][lane] = sacc[kb][qb];
+    // Every wave computes the same key reciprocals (lanes 32..63 repeat 0..31), so
+    // no wave waits on a branch here.
+    {
+      const int k = lane & (kBN - 1);
+      const float n = (sm.nxp[0][k] + sm.nxp[1][k]) + (sm.nxp[2][k] + sm.nxp[3][k]);
+      sm.rk[k] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
     }
   };
 
-  // t = 0: A only; then the query norms and A(0)'s publication.
-  stage_a(0);
+  // t = 0: A only, then the last tile of the ring's first round; the query norms and
+  // A(0)'s publication.
+  load_v(0, vv);
+  stage_a(0, IC<0>{});
+  wait_lds_reads();  // the query rows share slot R-1 with the tile fetched next
+  fetch_keys(R - 1, IC<R - 1>{});
   lds_barrier();
   if (tid < BM) {
     float ss = 0.f;
@@ -432,49 +546,75 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   }
   publish();
   lds_barrier();
-  for (int t = 1; t < nkt; ++t) {
+  // Steady state, unrolled by R so that every slot index is a constant. Iteration
+  // t reads tile t-1's mixing operands, refills its slot with tile t+R-1, and runs
+  // A(t) and B(t-1); then C(t-1) and A(t)'s publication.
+  auto iteration = [&](int t, auto cur) {
+    constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
+    stage_t(IC<PREV>{});
+    stage_a(t, cur);
+    wait_lds_reads();
+    fetch_keys(t + R - 1, IC<PREV>{});
     stage_b(t - 1);
-    stage_a(t);
     lds_barrier();
-    stage_c(t - 1);
+    stage_c();
     publish();
     lds_barrier();
+  };
+  int t = 1;
+  if constexpr (R == 2) {
+    for (; t + 1 < nkt; t += 2) {
+      iteration(t, IC<1>{});
+      iteration(t + 1, IC<0>{});
+    }
+    if (t < nkt) iteration(t, IC<1>{});
+  } else {
+    for (; t + 2 < nkt; t += 3) {
+      iteration(t, IC<1>{});
+      iteration(t + 1, IC<2>{});
+      iteration(t + 2, IC<0>{});
+    }
+    if (t < nkt) iteration(t, IC<1>{});
+    if (t + 1 < nkt) iteration(t + 1, IC<2>{});
   }
+  // Tail: the last tile's mixing operands; every slot is then free, so the gate rows
+  // stream into this wave's part of slots 0 / 1 while the last mixing product runs.
+  switch ((nkt - 1) % R) {
+    case 0: stage_t(IC<0>{}); break;
+    case 1: stage_t(IC<1>{}); break;
+    default: stage_t(IC<(R == 3 ? 2 : 0)>{}); break;
+  }
+  wait_lds_reads();
+  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
+  if (has_gate) fetch_rows(gb, erows_base);
   stage_b(nkt - 1);
   lds_barrier();
-  stage_c(nkt - 1);
+  stage_c();
 
   // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
-  // Gate rows, bias and row validity; rows past the context read as zero.
-  u32x2 gw[QB][NT];
+  uint32_t a3[G / 2];
+#pragma unroll
+  for (int m = 0; m < G / 2; ++m)
+    a3[m] = 16u * (uint32_t)(li * CPRP + swzc<G>(li, 2 * m + (lg >> 1))) + 8u * (uint32_t)(lg & 1);
+  auto efrag = [&](int qb, int t2) -> char* {
+    return erows_base(qb >> 1) + a3[t2 % (G / 2)] + 16 * (16 * (qb & 1) * CPRP + G * (t2 / (G / 2)));
+  };
   u32x2 bw[NT];
   uint32_t qv2[QB];
-  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
-  const uint32_t or_gate = has_gate ? 0u : (Ops<T16>::kOne | (Ops<T16>::kOne << 16));
-  const rsrc_t rbias = make_rsrc(has_bias ? p.bias : p.z, has_bias ? row_bytes : 0u);
-  uint32_t eoff[NT];
-#pragma unroll
-  for (int t2 = 0; t2 < NT; ++t2) {
-    const int f = fw + 16 * t2 + 4 * lg;
-    eoff[t2] = (FULL || f < D) ? (uint32_t)f * 2u : kNowhere;
-    bw[t2] = ld64(rbias, eoff[t2]);
-  }
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const rsrc_t rg = rows_rsrc(gb, q0 + 16 * qb, has_gate ? C : 0, row_bytes);
-    const rsrc_t rv = rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u);
-    qv2[qb] = ld8(rv, (uint32_t)li);
+  {
+    const rsrc_t rbias = make_rsrc(has_bias ? p.bias : p.z, has_bias ? row_bytes : 0u);
 #pragma unroll
     for (int t2 = 0; t2 < NT; ++t2) {
-      gw[qb][t2] = ld64(rg, (uint32_t)li * row_bytes + eoff[t2]);
-      gw[qb][t2] = u32x2{gw[qb][t2][0] | or_gate, gw[qb][t2][1] | or_gate};
+      const int f = fw + 16 * t2 + 4 * lg;
+      bw[t2] = ld64(rbias, (FULL || f < D) ? (uint32_t)f * 2u : kNowhere);
     }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
   }
   float rden[QB];
   if (p.normalize) {
 #pragma unroll
-    for (int j = 0; j < UPW; ++j)
-      if (UNITS % kWaves == 0 || w + kWaves * j < UNITS) sm.dx[uq[j]][uk[j]][lg][li] = den[j];
+    for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
     lds_barrier();
     if (tid < BM) {
       float d = 0.f;
@@ -491,28 +631,28 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) rden[qb] = 1.f;
   }
-  const rsrc_t rout_all = make_rsrc((char*)p.out + (int64_t)b * C * row_bytes, (uint32_t)C * row_bytes);
+  const uint32_t one2 = Ops<T16>::kOne | (Ops<T16>::kOne << 16);
+  // The result goes back into this wave's gate slots, then out in 16-byte runs.
   auto finish = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const int qrow = q0 + 16 * qb + li;
       const bool qok = (qv2[qb] | or_valid) != 0u;
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2) {
+        u32x2* e = reinterpret_cast<u32x2*>(efrag(qb, t2));
+        const u32x2 g2 = has_gate ? *e : u32x2{one2, one2};
         float y[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t bword = bw[t2][i >> 1], gword = gw[qb][t2][i >> 1];
+          const uint32_t bword = bw[t2][i >> 1], gword = g2[i >> 1];
           float x = oacc[t2][qb][i] * rden[qb];
           x += (i & 1) ? Ops<T16>::hi_f(bword) : Ops<T16>::to_f(bword & 0xffffu);
           x = activate<float>(x, ACT);
           x *= (i & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
           y[i] = qok ? x : 0.f;
         }
-        // Rows past the context fall outside rout_all and are dropped.
-        const uint32_t off = eoff[t2] == kNowhere ? kNowhere : (uint32_t)qrow * row_bytes + eoff[t2];
-        st64(u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])}, rout_all, off);
+        *e = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
       }
     }
   };
@@ -522,6 +662,13 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     case AVEY_ACT_SILU: finish(std::integral_constant<int, AVEY_ACT_SILU>{}); break;
     case AVEY_ACT_GELU: finish(std::integral_constant<int, AVEY_ACT_GELU>{}); break;
     default: finish(std::integral_constant<int, AVEY_ACT_IDENTITY>{}); break;
+  }
+  // Rows past the context fall outside the resources and are dropped.
+  const char* ob = (const char*)p.out + (int64_t)b * C * row_bytes;
+#pragma unroll
+  for (int j = 0; j < BM * CPRP / 64; ++j) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(erows_base(j / KDMA) + 1024 * (j % KDMA) + 16 * lane);
+    st128(v, rows_rsrc(ob, q0 + RPP * (j / P), C, row_bytes), kof[j % P]);
   }
 }
 
