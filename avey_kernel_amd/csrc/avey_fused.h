@@ -274,7 +274,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   f32x4(*const sx)[2][QB][64] = reinterpret_cast<f32x4(*)[2][QB][64]>(ovf);           // [wave][kb][qb][lane]
   u32x4(*const px)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX);                // [qb (QB: sink)][lane]
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // The wave index is read into a scalar register, so that LDS addresses built
+  // from it (DMA destinations go through M0) stay scalar.
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
   const int n_qt = (C + BM - 1) / BM;
@@ -317,9 +319,14 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     return (c < CPR && (FULL || col < D)) ? (uint32_t)r * row_bytes + (uint32_t)col * 2u : kNowhere;
   };
   constexpr int P = Gm::P, RPP = Gm::RPP;
-  uint32_t kof[P];
+  // The DMA lane offsets stay in registers unless the variant's registers are
+  // full (BM = 64 with 768-feature rows), where they are recomputed per tile.
+  constexpr bool KOF_LIVE = QB * NK < 24;
+  uint32_t kof_live[P];
+  if constexpr (KOF_LIVE) {
 #pragma unroll
-  for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
+    for (int j = 0; j < P; ++j) kof_live[j] = goff(64 * j + lane);
+  }
   // LDS byte offsets of this lane's fragments inside a slice (see Geo):
   //   a1: similarity operands, row li, chunk 4 s + lg          (s % (G / 4) picks the entry)
   //   a2: transposed mixing operands, row 4 lg + li / 4, chunk 2 t + (li & 3) / 2, half li & 1
@@ -362,19 +369,40 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   // bytes of its two 16-row blocks (rows past the context read 0 and are told apart
   // by their index). Tiles past the last are not fetched.
   uint32_t zv[R][2];
-  auto fetch_keys = [&](int t, auto slot) {
+  auto key_offsets = [&](uint32_t (&kof)[P]) {
+    if constexpr (KOF_LIVE) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) kof[j] = kof_live[j];
+    } else {
+      // Recomputed from an opaque lane index, so the compiler cannot keep them live.
+      const int ln = (int)opaque((uint32_t)lane);
+#pragma unroll
+      for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + ln);
+    }
+  };
+  // DMA instruction j (of KDMA) of key tile t into this wave's part of ring slot I.
+  auto fetch_key_part = [&](int t, auto slot, int j, const uint32_t (&kof)[P]) {
+    dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, row_bytes), slot_base(slot) + 1024 * j, kof[j % P]);
+  };
+  auto fetch_valid = [&](int t, auto slot) {
     constexpr int I = decltype(slot)::value;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, valid_rows, 1u), (uint32_t)li);
+  };
+  auto fetch_keys = [&](int t, auto slot) {
     if (t >= nkt) return;
-    const int k0 = t * kBN;
-    char* base = slot_base(slot);
+    uint32_t kof[P];
+    key_offsets(kof);
 #pragma unroll
-    for (int j = 0; j < KDMA; ++j) dma16(rows_rsrc(zb, k0 + RPP * (j / P), C, row_bytes), base + 1024 * j, kof[j % P]);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) zv[I][kb] = ld8(rows_rsrc(vb, k0 + 16 * kb, valid_rows, 1u), (uint32_t)li);
+    for (int j = 0; j < KDMA; ++j) fetch_key_part(t, slot, j, kof);
+    fetch_valid(t, slot);
   };
   // BM rows of a [B][C][D] tensor from row q0 into a row region (prologue: the
   // queries; epilogue: the gate).
   auto fetch_rows = [&](const char* src, auto region) {
+    uint32_t kof[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
 #pragma unroll
     for (int j = 0; j < BM * CPRP / 64; ++j)
       dma16(rows_rsrc(src, q0 + RPP * (j / P), C, row_bytes), region(j / KDMA) + 1024 * (j % KDMA), kof[j % P]);
@@ -435,11 +463,16 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
   };
 
-  // ---- A(t): partial similarity from slot I, key partial norms ------------------------
-  auto stage_a = [&](int t, auto slot) {
+  // ---- A(t): partial similarity from slot I, key partial norms; with FETCH, the
+  // refill of slot F with tile tf goes out one DMA per similarity step, so that a
+  // full memory queue stalls behind the MFMAs rather than in front of them --------------
+  auto stage_a = [&](int t, auto slot, int tf, auto fslot, auto fetch) {
     constexpr int I = decltype(slot)::value;
+    constexpr bool FETCH = decltype(fetch)::value;
     const int k0 = t * kBN;
     char* base = slot_base(slot);
+    uint32_t kof[P];
+    if constexpr (FETCH) key_offsets(kof);
     if (has_valid) {
       // Padded rows may hold NaN: once the tile has landed, zero them in this wave's
       // slice before they reach the products, the norms or the mixing operands.
@@ -468,9 +501,17 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
         ss = Ops<T16>::sumsq(a, ss);
+        if constexpr (FETCH) {
+          if (kb * NK + s < KDMA) fetch_key_part(tf, fslot, kb * NK + s, kof);
+        }
       }
       ss = sum_over_groups(ss);
       nkey[kb] = ok ? ss : -1.f;
+    }
+    if constexpr (FETCH) {
+#pragma unroll
+      for (int j = 2 * NK; j < KDMA; ++j) fetch_key_part(tf, fslot, j, kof);
+      fetch_valid(tf, fslot);
     }
     // Lane groups 0 / 1 write the two key halves (groups 2 / 3 repeat them).
     sm.nxp[w][16 * (lg & 1) + li] = (lg & 1) ? nkey[1] : nkey[0];
@@ -533,9 +574,11 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   // t = 0: A only, then the last tile of the ring's first round; the query norms and
   // A(0)'s publication.
   load_v(0, vv);
-  stage_a(0, IC<0>{});
-  wait_lds_reads();  // the query rows share slot R-1 with the tile fetched next
-  fetch_keys(R - 1, IC<R - 1>{});
+  // The query rows share slot R-1 with the tile fetched next; their reads into qf
+  // are complete (the norms above consumed them).
+  wait_lds_reads();
+  if (R - 1 < nkt) stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, std::true_type{});
+  else stage_a(0, IC<0>{}, 0, IC<R - 1>{}, std::false_type{});
   lds_barrier();
   if (tid < BM) {
     float ss = 0.f;
@@ -552,9 +595,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     stage_t(IC<PREV>{});
-    stage_a(t, cur);
-    wait_lds_reads();
-    fetch_keys(t + R - 1, IC<PREV>{});
+    wait_lds_reads();  // the refill below overwrites what stage_t read
+    if (t + R - 1 < nkt) stage_a(t, cur, t + R - 1, IC<PREV>{}, std::true_type{});
+    else stage_a(t, cur, 0, IC<PREV>{}, std::false_type{});
     stage_b(t - 1);
     lds_barrier();
     stage_c();
@@ -665,6 +708,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   }
   // Rows past the context fall outside the resources and are dropped.
   const char* ob = (const char*)p.out + (int64_t)b * C * row_bytes;
+  uint32_t kof[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
 #pragma unroll
   for (int j = 0; j < BM * CPRP / 64; ++j) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(erows_base(j / KDMA) + 1024 * (j % KDMA) + 16 * lane);
