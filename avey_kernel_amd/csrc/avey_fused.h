@@ -216,8 +216,22 @@ struct Geo {
   static constexpr int OVF = (BM > 32 && TILE > SX + PX) ? TILE : SX + PX;
   static constexpr int SMALL = 4 * (kWaves * kBN + kBN + kWaves * BM + BM + (QB + 1) * 2 * 4 * 16 + BM);
   static constexpr int kLdsMax = 160 * 1024;
-  // Ring depth: three slots when they fit, else two.
-  static constexpr int R = (3 * TILE + OVF + SMALL <= kLdsMax) ? 3 : 2;
+  // A BM-row region of its own (the gate rows): each wave's rows in groups of
+  // GROWS rows, GSL bytes per group.
+  static constexpr int GROWS = BM < kBN ? BM : kBN;
+  static constexpr int GSL = GROWS * CPRP * 16;
+  static constexpr int QREG = BM * CPRP * 64;
+  static_assert((BM / GROWS) * kWaves * GSL == QREG, "gate region layout");
+  // Ring depth and gate placement, the first that fits: three slots and a gate
+  // region of its own (the gate is then fetched two tiles before the end), three
+  // slots, two slots and a gate region, two slots (the gate then streams into the
+  // ring once the last tile has been read). The third slot comes first: on the
+  // 768-feature causal shape it is worth more than an early gate.
+  static constexpr bool kFit3G = 3 * TILE + OVF + QREG + SMALL <= kLdsMax;
+  static constexpr bool kFit3 = 3 * TILE + OVF + SMALL <= kLdsMax;
+  static constexpr bool kFit2G = 2 * TILE + OVF + QREG + SMALL <= kLdsMax;
+  static constexpr int R = (kFit3G || kFit3) ? 3 : 2;
+  static constexpr bool EARLY_GATE = kFit3G || (!kFit3 && kFit2G);
   static_assert(2 * TILE + OVF + SMALL <= kLdsMax, "tile does not fit the LDS");
   static_assert(BM <= 32 * R, "query rows must fit the ring");
 };
@@ -270,6 +284,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(16))) char slot1[TILE];
   __shared__ __attribute__((aligned(16))) char slot2[R == 3 ? TILE : 16];
   __shared__ __attribute__((aligned(16))) char ovf[Gm::OVF];
+  __shared__ __attribute__((aligned(16))) char grows[Gm::EARLY_GATE ? Gm::QREG : 16];
   __shared__ SmallLds<BM> sm;
   f32x4(*const sx)[2][QB][64] = reinterpret_cast<f32x4(*)[2][QB][64]>(ovf);           // [wave][kb][qb][lane]
   u32x4(*const px)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX);                // [qb (QB: sink)][lane]
@@ -309,7 +324,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     return s + w * SLICE;
   };
   auto qrows_base = [&](int j) -> char* { return j == 0 ? ((R == 3 ? slot2 : slot1) + w * SLICE) : (ovf + w * SLICE); };
-  auto erows_base = [&](int j) -> char* { return (j == 0 ? slot0 : slot1) + w * SLICE; };
+  auto erows_base = [&](int j) -> char* {
+    if constexpr (Gm::EARLY_GATE) return grows + (j * kWaves + w) * Gm::GSL;
+    else return (j == 0 ? slot0 : slot1) + w * SLICE;
+  };
 
   // Global byte offset (from a region's first row) of slice position pos, i.e. row
   // pos / CPRP, chunk swizzle(row, pos % CPRP); kNowhere past the slice or past D.
@@ -417,10 +435,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
       for (int i = 0; i < 4; ++i) vv[j][i] = ld16(r, voff[j] + 2u * (uint32_t)i);
   };
 
-  // ---- prologue: the first R-1 key tiles, the query rows and their norms ------------
+  // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
+  fetch_rows((const char*)zb, qrows_base);
   fetch_keys(0, IC<0>{});
   if constexpr (R == 3) fetch_keys(1, IC<1>{});
-  fetch_rows((const char*)zb, qrows_base);
   uint32_t qv[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
@@ -591,7 +609,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
   // t reads tile t-1's mixing operands, refills its slot with tile t+R-1, and runs
-  // A(t) and B(t-1); then C(t-1) and A(t)'s publication.
+  // A(t) and B(t-1); then C(t-1) and A(t)'s publication. With a gate region of its
+  // own, the gate rows are fetched two tiles before the end.
+  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
+  const int gate_t = nkt > 3 ? nkt - 2 : 1;
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     stage_t(IC<PREV>{});
@@ -599,6 +620,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if (t + R - 1 < nkt) stage_a(t, cur, t + R - 1, IC<PREV>{}, std::true_type{});
     else stage_a(t, cur, 0, IC<PREV>{}, std::false_type{});
     stage_b(t - 1);
+    if constexpr (Gm::EARLY_GATE) {
+      if (has_gate && t == gate_t) fetch_rows(gb, erows_base);
+    }
     lds_barrier();
     stage_c();
     publish();
@@ -620,16 +644,16 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if (t < nkt) iteration(t, IC<1>{});
     if (t + 1 < nkt) iteration(t + 1, IC<2>{});
   }
-  // Tail: the last tile's mixing operands; every slot is then free, so the gate rows
-  // stream into this wave's part of slots 0 / 1 while the last mixing product runs.
+  // Tail: the last tile's mixing operands; every slot is then free, so without a
+  // gate region the gate rows stream into this wave's part of slots 0 / 1 while the
+  // last mixing product runs.
   switch ((nkt - 1) % R) {
     case 0: stage_t(IC<0>{}); break;
     case 1: stage_t(IC<1>{}); break;
     default: stage_t(IC<(R == 3 ? 2 : 0)>{}); break;
   }
   wait_lds_reads();
-  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
-  if (has_gate) fetch_rows(gb, erows_base);
+  if (has_gate && (!Gm::EARLY_GATE || nkt == 1)) fetch_rows(gb, erows_base);
   stage_b(nkt - 1);
   lds_barrier();
   stage_c();

@@ -270,3 +270,58 @@ def test_hip_graph_replay_matches_eager():
         # Eager work between replays.
         _ = wl.call(cfg, inp)
         torch.cuda.synchronize()
+
+
+# Every compiled fused variant: query-tile height BM in {16, 32, 64} (forced through
+# the grid-size rule of the static tile table) x wave-slice width 32 * NK for
+# NK in {1, 2, 3, 4, 6, 8}, with whole slices (D == 128 NK) and with a partial last
+# slice. (batch, context) pairs pick BM: the table starts at 64 (32 for NK = 8) and
+# halves while the grid has fewer than 256 workgroups.
+_BM_SHAPES = {16: (2, 70), 32: (32, 256), 64: (64, 256)}
+_VARIANTS = [(bm, d) for bm in (16, 32, 64)
+             for d in (128, 120, 256, 200, 384, 328, 512, 456, 768, 640, 1024, 1000)
+             if not (bm == 64 and d > 768)]
+
+
+@pytest.mark.parametrize('bm,d', _VARIANTS, ids=lambda x: str(x))
+def test_every_fused_variant_matches_oracle(bm, d):
+    batch, context = _BM_SHAPES[bm]
+    if bm == 32 and d > 768:
+        batch, context = 64, 256  # NK = 8 starts at BM = 32
+    plan = _hip.plan((batch, context, d), torch.bfloat16, causal=True, normalize=False)
+    nk = -(-d // 128)
+    nk = nk if nk <= 4 else (6 if nk <= 6 else 8)
+    assert plan['kernel'] == 'fused_mfma' and plan['block_m'] == bm and plan['block_d'] == 32 * nk, plan
+    g = torch.Generator().manual_seed(bm * 1000 + d)
+    z = torch.randn(batch, context, d, generator=g)
+    gate = torch.randn(batch, context, d, generator=g)
+    bias = torch.randn(d, generator=g) * 0.1
+    v = (torch.rand(context, context, generator=g) * 2 - 1) / context ** 0.5
+    # Ragged key padding with NaN in the padded rows (one batch item unpadded).
+    lengths = torch.randint(context // 2, context + 1, (batch,), generator=g)
+    lengths[0] = context
+    valid = torch.arange(context)[None, :] < lengths[:, None]
+    z_nan = z.clone()
+    z_nan[~valid] = float('nan')
+    zb, gb, bb, vb = (t.to(DEV, torch.bfloat16) for t in (z, gate, bias, v))
+    znb = z_nan.to(DEV, torch.bfloat16)
+    validd = valid.to(DEV)
+    acc = np.float64 if batch * context * context * d < 5e8 else np.float32
+    cases = [
+        ('avey causal', dict(v=vb, normalize=False, causal=True, valid=None, eps=1e-6, act='silu', z=zb)),
+        ('avey_b padded NaN', dict(v=None, normalize=True, causal=False, valid=validd, eps=0.25, act='gelu', z=znb)),
+        ('avey bidirectional padded', dict(v=vb, normalize=False, causal=False, valid=validd, eps=1e-6,
+                                           act='identity', z=znb)),
+    ]
+    for label, c in cases:
+        out = _fused(c['z'], c['v'], gb, bb, c['valid'], eps=c['eps'], causal=c['causal'], normalize=c['normalize'],
+                     act=c['act'])
+        zc = c['z'] if c['valid'] is None else zb  # the oracle zeroes padded rows itself; feed it finite ones
+        want = _oracle(zc, c['v'], gb, bb, c['valid'], eps=c['eps'], causal=c['causal'], normalize=c['normalize'],
+                       act=c['act'], acc=acc)
+        cond = None
+        if c['normalize']:
+            cond = orc.row_condition(_np(zc), None if c['valid'] is None else valid.numpy(), eps=c['eps'])
+        _assert_close(out, want, torch.bfloat16, f'BM{bm} D{d} {label}', cond)
+        if c['valid'] is not None:
+            assert torch.all(out[~validd] == 0), f'BM{bm} D{d} {label}: padded rows not zero'
