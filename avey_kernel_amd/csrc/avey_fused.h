@@ -179,12 +179,18 @@ __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
 }
 
-// Workgroup barrier that orders LDS only: global loads stay in flight across it
-// (__syncthreads() would also wait for every outstanding global load).
+// Workgroup barrier for the LDS exchanges between waves (partial similarities,
+// P, norms): the wave's own LDS accesses complete first (lgkmcnt(0)), and memory
+// clobbers keep the compiler from moving LDS accesses across it. Global loads and
+// the buffer-to-LDS copies stay in flight: a workgroup-scope LDS fence would
+// also wait for every copy (they write LDS), but each wave only ever reads the
+// copies it issued itself, and the compiler's own wait before those reads covers
+// them.
 __device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  asm volatile("" ::: "memory");
 }
 
 // LDS-geometry of one (BM, NK) variant. Key tiles, the query rows and the gate
@@ -608,18 +614,20 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   publish();
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
-  // t reads tile t-1's mixing operands, refills its slot with tile t+R-1, and runs
-  // A(t) and B(t-1); then C(t-1) and A(t)'s publication. With a gate region of its
-  // own, the gate rows are fetched two tiles before the end.
+  // t reads tile t-1's mixing operands, runs B(t-1), then A(t) while refilling
+  // tile t-1's slot with tile t+R-1; then C(t-1) and A(t)'s publication. With a
+  // gate region of its own, the gate rows are fetched two tiles before the end.
   const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
   const int gate_t = nkt > 3 ? nkt - 2 : 1;
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     stage_t(IC<PREV>{});
+    // B first: the V words it consumes were loaded before this iteration's DMAs, so
+    // waiting for them (vmcnt counts in issue order) never waits for the refill.
+    stage_b(t - 1);
     wait_lds_reads();  // the refill below overwrites what stage_t read
     if (t + R - 1 < nkt) stage_a(t, cur, t + R - 1, IC<PREV>{}, std::true_type{});
     else stage_a(t, cur, 0, IC<PREV>{}, std::false_type{});
-    stage_b(t - 1);
     if constexpr (Gm::EARLY_GATE) {
       if (has_gate && t == gate_t) fetch_rows(gb, erows_base);
     }
