@@ -28,6 +28,14 @@ HIP_FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
              '-Wno-pass-failed', '-I', INCLUDE, '-I', CSRC]
 
 
+# Accumulators of the 16- and 32-row fused variants fit the 256 architectural VGPRs;
+# with MFMA results in VGPRs the compiler stops shuttling them through AGPRs
+# (hundreds of v_accvgpr moves per key tile otherwise). The 64-row variants need
+# more than 256 registers and keep the compiler's default split.
+EXTRA_FLAGS = {f'avey_fused_bm{bm}_{t}.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']
+               for bm in (16, 32) for t in ('bf16', 'f16')}
+
+
 def hipcc():
     path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
     if not os.path.exists(path):
@@ -37,7 +45,7 @@ def hipcc():
 
 def _compile(src):
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + '.o')
-    cmd = [hipcc(), *HIP_FLAGS, '-c', os.path.join(CSRC, src), '-o', obj]
+    cmd = [hipcc(), *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), '-c', os.path.join(CSRC, src), '-o', obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed for {src}:\n{res.stderr}')

@@ -138,7 +138,6 @@ template <> struct Ops<__bf16> {
   // to_f(u | one): `one` is 0 or kOne, so an all-zero word can stand for 1.0.
   __device__ static float to_f_or(uint32_t u, uint32_t one) { return __uint_as_float((u | one) << 16); }
   __device__ static float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-  __device__ static uint32_t from_f(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x); }
 };
 template <> struct Ops<_Float16> {
   static constexpr uint32_t kOne = 0x3c00u;
@@ -158,12 +157,16 @@ template <> struct Ops<_Float16> {
   __device__ static float to_f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
   __device__ static float to_f_or(uint32_t u, uint32_t one) { return to_f(u | one); }
   __device__ static float hi_f(uint32_t w) { return to_f(w >> 16); }
-  __device__ static uint32_t from_f(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x); }
 };
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded (to nearest even) into one word, lo in the low half: a single
+// v_cvt_pk_{bf16,f16}_f32.
 template <typename T16>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return Ops<T16>::from_f(lo) | (Ops<T16>::from_f(hi) << 16);
+  typedef T16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), h2));
 }
 
 // Sum of a value over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48),
@@ -222,22 +225,8 @@ struct Geo {
   static constexpr int OVF = (BM > 32 && TILE > SX + PX) ? TILE : SX + PX;
   static constexpr int SMALL = 4 * (kWaves * kBN + kBN + kWaves * BM + BM + (QB + 1) * 2 * 4 * 16 + BM);
   static constexpr int kLdsMax = 160 * 1024;
-  // A BM-row region of its own (the gate rows): each wave's rows in groups of
-  // GROWS rows, GSL bytes per group.
-  static constexpr int GROWS = BM < kBN ? BM : kBN;
-  static constexpr int GSL = GROWS * CPRP * 16;
-  static constexpr int QREG = BM * CPRP * 64;
-  static_assert((BM / GROWS) * kWaves * GSL == QREG, "gate region layout");
-  // Ring depth and gate placement, the first that fits: three slots and a gate
-  // region of its own (the gate is then fetched two tiles before the end), three
-  // slots, two slots and a gate region, two slots (the gate then streams into the
-  // ring once the last tile has been read). The third slot comes first: on the
-  // 768-feature causal shape it is worth more than an early gate.
-  static constexpr bool kFit3G = 3 * TILE + OVF + QREG + SMALL <= kLdsMax;
-  static constexpr bool kFit3 = 3 * TILE + OVF + SMALL <= kLdsMax;
-  static constexpr bool kFit2G = 2 * TILE + OVF + QREG + SMALL <= kLdsMax;
-  static constexpr int R = (kFit3G || kFit3) ? 3 : 2;
-  static constexpr bool EARLY_GATE = kFit3G || (!kFit3 && kFit2G);
+  // Ring depth: three slots where they fit, else two.
+  static constexpr int R = 3 * TILE + OVF + SMALL <= kLdsMax ? 3 : 2;
   static_assert(2 * TILE + OVF + SMALL <= kLdsMax, "tile does not fit the LDS");
   static_assert(BM <= 32 * R, "query rows must fit the ring");
 };
@@ -255,7 +244,12 @@ __device__ __forceinline__ int swzc(int r, int c) {
 template <int BM>
 struct SmallLds {
   float nxp[kWaves][kBN];            // per-wave partial sums of squares of the keys; -1: padded key
-  float rk[kBN];                     // 1 / max(||k||, norm_eps); 0 for padded or out-of-range keys
+  // 1 / max(||k||, norm_eps) of key 4 i + j in rk[i][j]; 0 for padded or out-of-range
+  // keys. Stored as 16-byte vectors so the four a lane reads are one aligned load: an
+  // under-aligned vector load is split, and the split accesses lose the alias scopes
+  // that tell the compiler they cannot overlap a buffer-to-LDS copy in flight (it
+  // would then wait for every copy before them).
+  f32x4 rk[kBN / 4];
   float nq[kWaves][BM];              // per-wave partial sums of squares of the queries
   float rq[BM];                      // 1 / max(||q||, norm_eps); 0 for padded or out-of-range rows
   float dx[BM / 16 + 1][2][4][16];   // signed row-sum partials; last row: sink of idle waves
@@ -265,6 +259,10 @@ struct SmallLds {
 // Global -> LDS copy of 16 bytes per lane: lane l's bytes land at lds + 16 l.
 __device__ __forceinline__ void dma16(rsrc_t r, char* lds, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
+// Global -> LDS copy of 4 bytes per lane (lane l's word lands at lds + 4 l).
+__device__ __forceinline__ void dma4(rsrc_t r, char* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, off, 0, 0, 0);
 }
 __device__ __forceinline__ void st128(u32x4 v, rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
@@ -290,8 +288,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(16))) char slot1[TILE];
   __shared__ __attribute__((aligned(16))) char slot2[R == 3 ? TILE : 16];
   __shared__ __attribute__((aligned(16))) char ovf[Gm::OVF];
-  __shared__ __attribute__((aligned(16))) char grows[Gm::EARLY_GATE ? Gm::QREG : 16];
   __shared__ SmallLds<BM> sm;
+  // Landing place of the cache-line touches below; never read.
+  __shared__ __attribute__((aligned(16))) char touch_sink[256];
+  static_assert(sizeof(SmallLds<BM>) <= Gm::SMALL, "small LDS arrays");
   f32x4(*const sx)[2][QB][64] = reinterpret_cast<f32x4(*)[2][QB][64]>(ovf);           // [wave][kb][qb][lane]
   u32x4(*const px)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX);                // [qb (QB: sink)][lane]
 
@@ -308,6 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   const char* zb = (const char*)p.z + (int64_t)b * C * row_bytes;
   const bool has_valid = p.valid != nullptr, has_v = p.v != nullptr;
   const bool has_gate = p.gate != nullptr, has_bias = p.bias != nullptr;
+  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
   // Absent operands get empty resources (their loads read 0); `or_*` turns those
   // zeros into the neutral value where 0 is not neutral.
   const char* vb = has_valid ? (const char*)p.valid + (int64_t)b * C : (const char*)p.z;
@@ -323,17 +324,15 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 
   // ---- addressing -------------------------------------------------------------------
   // This wave's part of ring slot I, and row group j (32 rows) of the query region
-  // (prologue) and of the gate / output region (epilogue).
+  // (prologue) and of the gate / output region (epilogue). Key tile t sits in slot
+  // t % R.
   auto slot_base = [&](auto slot) -> char* {
     constexpr int I = decltype(slot)::value;
     char* s = I == 0 ? slot0 : (I == 1 ? slot1 : slot2);
     return s + w * SLICE;
   };
   auto qrows_base = [&](int j) -> char* { return j == 0 ? ((R == 3 ? slot2 : slot1) + w * SLICE) : (ovf + w * SLICE); };
-  auto erows_base = [&](int j) -> char* {
-    if constexpr (Gm::EARLY_GATE) return grows + (j * kWaves + w) * Gm::GSL;
-    else return (j == 0 ? slot0 : slot1) + w * SLICE;
-  };
+  auto erows_base = [&](int j) -> char* { return (j == 0 ? slot0 : slot1) + w * SLICE; };
 
   // Global byte offset (from a region's first row) of slice position pos, i.e. row
   // pos / CPRP, chunk swizzle(row, pos % CPRP); kNowhere past the slice or past D.
@@ -404,9 +403,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
       for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + ln);
     }
   };
-  // DMA instruction j (of KDMA) of key tile t into this wave's part of ring slot I.
-  auto fetch_key_part = [&](int t, auto slot, int j, const uint32_t (&kof)[P]) {
-    dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, row_bytes), slot_base(slot) + 1024 * j, kof[j % P]);
+  // DMA instruction j (of KDMA) of key tile t into this wave's part of a ring slot.
+  auto fetch_key_part = [&](int t, char* dst, int j, const uint32_t (&kof)[P]) {
+    dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, row_bytes), dst + 1024 * j, kof[j % P]);
   };
   auto fetch_valid = [&](int t, auto slot) {
     constexpr int I = decltype(slot)::value;
@@ -414,15 +413,14 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     for (int kb = 0; kb < 2; ++kb) zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, valid_rows, 1u), (uint32_t)li);
   };
   auto fetch_keys = [&](int t, auto slot) {
-    if (t >= nkt) return;
     uint32_t kof[P];
     key_offsets(kof);
 #pragma unroll
-    for (int j = 0; j < KDMA; ++j) fetch_key_part(t, slot, j, kof);
+    for (int j = 0; j < KDMA; ++j) fetch_key_part(t, slot_base(slot), j, kof);
     fetch_valid(t, slot);
   };
   // BM rows of a [B][C][D] tensor from row q0 into a row region (prologue: the
-  // queries; epilogue: the gate).
+  // queries; tail: the gate).
   auto fetch_rows = [&](const char* src, auto region) {
     uint32_t kof[P];
 #pragma unroll
@@ -444,7 +442,17 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
   fetch_rows((const char*)zb, qrows_base);
   fetch_keys(0, IC<0>{});
-  if constexpr (R == 3) fetch_keys(1, IC<1>{});
+  if constexpr (R == 3) {
+    if (1 < nkt) fetch_keys(1, IC<1>{});
+  }
+  // The gate rows are first read at the end; one touch per 128-byte line now brings
+  // them into the L2, so that their fetch in the tail does not wait on HBM.
+  if (has_gate) {
+    const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), row_bytes);
+    constexpr int kTouches = (BM * 4 * 32 * NK * 2 / 128 + kThreads - 1) / kThreads;  // lines over 256 lanes
+#pragma unroll
+    for (int i = 0; i < kTouches; ++i) dma4(r, touch_sink, (uint32_t)(i * kThreads + tid) * 128u);
+  }
   uint32_t qv[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
@@ -488,8 +496,8 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   };
 
   // ---- A(t): partial similarity from slot I, key partial norms; with FETCH, the
-  // refill of slot F with tile tf goes out one DMA per similarity step, so that a
-  // full memory queue stalls behind the MFMAs rather than in front of them --------------
+  // refill of slot F with key tile tf goes out one DMA per similarity step, so that
+  // a full memory queue stalls behind the MFMAs rather than in front of them ---------
   auto stage_a = [&](int t, auto slot, int tf, auto fslot, auto fetch) {
     constexpr int I = decltype(slot)::value;
     constexpr bool FETCH = decltype(fetch)::value;
@@ -526,7 +534,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
         for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
         ss = Ops<T16>::sumsq(a, ss);
         if constexpr (FETCH) {
-          if (kb * NK + s < KDMA) fetch_key_part(tf, fslot, kb * NK + s, kof);
+          if (kb * NK + s < KDMA) fetch_key_part(tf, slot_base(fslot), kb * NK + s, kof);
         }
       }
       ss = sum_over_groups(ss);
@@ -534,7 +542,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
     if constexpr (FETCH) {
 #pragma unroll
-      for (int j = 2 * NK; j < KDMA; ++j) fetch_key_part(tf, fslot, j, kof);
+      for (int j = 2 * NK; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
       fetch_valid(tf, fslot);
     }
     // Lane groups 0 / 1 write the two key halves (groups 2 / 3 repeat them).
@@ -552,7 +560,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
       f32x4 sv = sx[0][kb][qb][lane];
 #pragma unroll
       for (int x = 1; x < kWaves; ++x) sv += sx[x][kb][qb][lane];
-      const f32x4 rk4 = *reinterpret_cast<const f32x4*>(&sm.rk[16 * kb + 4 * lg]);
+      const f32x4 rk4 = sm.rk[4 * kb + lg];
       const float rqv = sm.rq[16 * qb + li];  // 0 for padded / out-of-range queries
       float pv[4];
 #pragma unroll
@@ -591,7 +599,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     {
       const int k = lane & (kBN - 1);
       const float n = (sm.nxp[0][k] + sm.nxp[1][k]) + (sm.nxp[2][k] + sm.nxp[3][k]);
-      sm.rk[k] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
+      // A float store: an element assignment to the vector would be a read-modify-
+      // write of all 16 bytes, racing with the lanes that own the other three keys.
+      reinterpret_cast<float*>(sm.rk)[k] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
     }
   };
 
@@ -615,10 +625,8 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
   // t reads tile t-1's mixing operands, runs B(t-1), then A(t) while refilling
-  // tile t-1's slot with tile t+R-1; then C(t-1) and A(t)'s publication. With a
-  // gate region of its own, the gate rows are fetched two tiles before the end.
-  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
-  const int gate_t = nkt > 3 ? nkt - 2 : 1;
+  // tile t-1's slot with ring tile t+R-1 (a key tile, or past the last one the gate
+  // rows); then C(t-1) and A(t)'s publication.
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     stage_t(IC<PREV>{});
@@ -628,9 +636,6 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     wait_lds_reads();  // the refill below overwrites what stage_t read
     if (t + R - 1 < nkt) stage_a(t, cur, t + R - 1, IC<PREV>{}, std::true_type{});
     else stage_a(t, cur, 0, IC<PREV>{}, std::false_type{});
-    if constexpr (Gm::EARLY_GATE) {
-      if (has_gate && t == gate_t) fetch_rows(gb, erows_base);
-    }
     lds_barrier();
     stage_c();
     publish();
@@ -652,16 +657,16 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if (t < nkt) iteration(t, IC<1>{});
     if (t + 1 < nkt) iteration(t + 1, IC<2>{});
   }
-  // Tail: the last tile's mixing operands; every slot is then free, so without a
-  // gate region the gate rows stream into this wave's part of slots 0 / 1 while the
-  // last mixing product runs.
+  // Tail: the last tile's mixing operands; every slot is then free, and the gate rows
+  // (already in the L2) stream into this wave's part of slots 0 / 1 while the last
+  // reduction and mixing product run.
   switch ((nkt - 1) % R) {
     case 0: stage_t(IC<0>{}); break;
     case 1: stage_t(IC<1>{}); break;
     default: stage_t(IC<(R == 3 ? 2 : 0)>{}); break;
   }
   wait_lds_reads();
-  if (has_gate && (!Gm::EARLY_GATE || nkt == 1)) fetch_rows(gb, erows_base);
+  if (has_gate) fetch_rows(gb, erows_base);
   stage_b(nkt - 1);
   lds_barrier();
   stage_c();
@@ -707,27 +712,37 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     for (int qb = 0; qb < QB; ++qb) rden[qb] = 1.f;
   }
   const uint32_t one2 = Ops<T16>::kOne | (Ops<T16>::kOne << 16);
-  // The result goes back into this wave's gate slots, then out in 16-byte runs.
+  // The result goes back into this wave's gate slots, then out in 16-byte runs. The
+  // gate words of up to 12 fragments are read before any result is written: the
+  // compiler cannot tell the reads from the writes apart, and interleaved they
+  // would pay one LDS round trip each.
+  constexpr int GB = NT <= 12 ? NT : 8;
   auto finish = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const bool qok = (qv2[qb] | or_valid) != 0u;
 #pragma unroll
-      for (int t2 = 0; t2 < NT; ++t2) {
-        u32x2* e = reinterpret_cast<u32x2*>(efrag(qb, t2));
-        const u32x2 g2 = has_gate ? *e : u32x2{one2, one2};
-        float y[4];
+      for (int tb = 0; tb < NT; tb += GB) {
+        u32x2 gw[GB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t bword = bw[t2][i >> 1], gword = g2[i >> 1];
-          float x = oacc[t2][qb][i] * rden[qb];
-          x += (i & 1) ? Ops<T16>::hi_f(bword) : Ops<T16>::to_f(bword & 0xffffu);
-          x = activate<float>(x, ACT);
-          x *= (i & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
-          y[i] = qok ? x : 0.f;
+        for (int i = 0; i < GB; ++i)
+          gw[i] = has_gate ? *reinterpret_cast<const u32x2*>(efrag(qb, tb + i)) : u32x2{one2, one2};
+#pragma unroll
+        for (int i = 0; i < GB; ++i) {
+          const int t2 = tb + i;
+          float y[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t bword = bw[t2][k >> 1], gword = gw[i][k >> 1];
+            float x = oacc[t2][qb][k] * rden[qb];
+            x += (k & 1) ? Ops<T16>::hi_f(bword) : Ops<T16>::to_f(bword & 0xffffu);
+            x = activate<float>(x, ACT);
+            x *= (k & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
+            y[k] = qok ? x : 0.f;
+          }
+          *reinterpret_cast<u32x2*>(efrag(qb, t2)) = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
         }
-        *e = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
       }
     }
   };
