@@ -90,11 +90,11 @@ __device__ __forceinline__ rsrc_t rows_rsrc(const char* base, int row0, int rows
 __device__ __forceinline__ u32x4 ld128(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
-__device__ __forceinline__ u32x2 ld64(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-}
 __device__ __forceinline__ uint32_t ld16(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 ld64(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
 __device__ __forceinline__ uint32_t ld8(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
@@ -429,14 +429,22 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     for (int j = 0; j < BM * CPRP / 64; ++j)
       dma16(rows_rsrc(src, q0 + RPP * (j / P), C, row_bytes), region(j / KDMA) + 1024 * (j % KDMA), kof[j % P]);
   };
-  // V entries of tile k0 for this wave's units (raw 16-bit words).
-  auto load_v = [&](int k0, uint32_t (&vv)[UPW][4]) {
+  // V entries of tile k0 for this wave's units (raw 16-bit words, two per dword): the
+  // lane's four keys are adjacent, so with an even context one dword-aligned 8-byte
+  // load fetches them. With an odd one a row may start mid-dword, and V's last dword
+  // is half past its end (a buffer load reads such a dword as 0), so the entries are
+  // then read one by one. Entries past the end of V read 0; their keys are masked.
+  auto load_v = [&](int k0, u32x2 (&vv)[UPW]) {
     const uint32_t skip = (uint32_t)k0 * 2u;
     const rsrc_t r = make_rsrc((const char*)(has_v ? p.v : p.z) + skip, vbytes > skip ? vbytes - skip : 0u);
+    if ((C & 1) == 0) {
 #pragma unroll
-    for (int j = 0; j < UPW; ++j)
+      for (int j = 0; j < UPW; ++j) vv[j] = ld64(r, voff[j]);
+    } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vv[j][i] = ld16(r, voff[j] + 2u * (uint32_t)i);
+      for (int j = 0; j < UPW; ++j)
+        vv[j] = u32x2{ld16(r, voff[j]) | (ld16(r, voff[j] + 2u) << 16), ld16(r, voff[j] + 4u) | (ld16(r, voff[j] + 6u) << 16)};
+    }
   };
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
@@ -480,7 +488,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
   for (int j = 0; j < UPW; ++j) den[j] = 0.f;
   f32x4 sacc[2][QB];
-  uint32_t vv[UPW][4];
+  u32x2 vv[UPW];
   u32x4 ztr[NT];  // transposed mixing operands of the previous tile
 
   // ---- T(t): the mixing operands of tile t, read transposed from its slot -------------
@@ -495,16 +503,23 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
   };
 
-  // ---- A(t): partial similarity from slot I, key partial norms; with FETCH, the
-  // refill of slot F with key tile tf goes out one DMA per similarity step, so that
-  // a full memory queue stalls behind the MFMAs rather than in front of them ---------
-  auto stage_a = [&](int t, auto slot, int tf, auto fslot, auto fetch) {
+  // ---- A(t): partial similarity from slot I, key partial norms. When `refill`, the
+  // refill of slot F with key tile tf goes out interleaved with MFMAs, so that the
+  // memory queue drains behind them instead of stalling the wave: with at most 32
+  // query rows it is spread thinly over A and C (one DMA every other MFMA; A issues
+  // [0, KA), C the rest), while the 64-row variants, whose registers are full, keep
+  // it in A, one DMA per step. A issues DMAs [0, JE). The DMAs sit under their own
+  // uniform branches, so the MFMA code is not duplicated.
+  constexpr bool SPLIT = BM <= 32;
+  constexpr int KA = SPLIT ? (KDMA + 1) / 2 : KDMA;
+  constexpr int SP = SPLIT ? 2 : 1;  // MFMA steps per DMA in A
+  auto stage_a = [&](int t, auto slot, int tf, auto fslot, bool refill, auto je) {
     constexpr int I = decltype(slot)::value;
-    constexpr bool FETCH = decltype(fetch)::value;
+    constexpr int JE = decltype(je)::value;
     const int k0 = t * kBN;
     char* base = slot_base(slot);
     uint32_t kof[P];
-    if constexpr (FETCH) key_offsets(kof);
+    key_offsets(kof);
     if (has_valid) {
       // Padded rows may hold NaN: once the tile has landed, zero them in this wave's
       // slice before they reach the products, the norms or the mixing operands.
@@ -533,17 +548,16 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
         ss = Ops<T16>::sumsq(a, ss);
-        if constexpr (FETCH) {
-          if (kb * NK + s < KDMA) fetch_key_part(tf, slot_base(fslot), kb * NK + s, kof);
-        }
+        const int step = kb * NK + s;
+        if (step % SP == 0 && step / SP < JE && refill) fetch_key_part(tf, slot_base(fslot), step / SP, kof);
       }
       ss = sum_over_groups(ss);
       nkey[kb] = ok ? ss : -1.f;
     }
-    if constexpr (FETCH) {
+    if (refill) {
 #pragma unroll
-      for (int j = 2 * NK; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
-      fetch_valid(tf, fslot);
+      for (int j = (2 * NK + SP - 1) / SP; j < JE; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
+      if constexpr (JE == KDMA) fetch_valid(tf, fslot);
     }
     // Lane groups 0 / 1 write the two key halves (groups 2 / 3 repeat them).
     sm.nxp[w][16 * (lg & 1) + li] = (lg & 1) ? nkey[1] : nkey[0];
@@ -568,7 +582,8 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
         // Causal and key-padding masks (padded / out-of-range keys have rk == 0) as
         // bitwise selects: whatever V holds there, the entry is an exact +0.
         const uint32_t keep = ((ud[j] + (float)i <= lim) & (rk4[i] > 0.f)) ? 0xffffffffu : 0u;
-        const float x = sv[i] * (rk4[i] * rqv) * Ops<T16>::to_f_or(vv[j][i], or_v);
+        const uint32_t vw = vv[j][i >> 1];
+        const float x = sv[i] * (rk4[i] * rqv) * Ops<T16>::to_f_or((i & 1) ? vw >> 16 : vw & 0xffffu, or_v);
         pv[i] = __uint_as_float(__float_as_uint(x) & keep);
         den[j] += pv[i];
       }
@@ -577,15 +592,28 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     load_v(t + 1 < nkt ? (t + 1) * kBN : C, vv);
   };
 
-  // ---- C: mixing of the previous tile from the transposed operands in registers ---------
-  auto stage_c = [&]() {
+  // ---- C: mixing of the previous tile from the transposed operands in registers; with
+  // FETCH, the second part of the refill A started (one DMA every other MFMA) ------------
+  auto stage_c = [&](int tf, auto fslot, bool refill) {
+    if constexpr (!SPLIT) refill = false;
+    uint32_t kof[P];
+    if constexpr (SPLIT) key_offsets(kof);
     u32x4 pf[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) pf[qb] = px[qb][lane];
 #pragma unroll
     for (int t2 = 0; t2 < NT; ++t2)
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pf[qb], oacc[t2][qb]);
+      for (int qb = 0; qb < QB; ++qb) {
+        oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pf[qb], oacc[t2][qb]);
+        const int m = t2 * QB + qb;
+        if (m % 2 == 0 && KA + m / 2 < KDMA && refill) fetch_key_part(tf, slot_base(fslot), KA + m / 2, kof);
+      }
+    if (refill) {
+#pragma unroll
+      for (int j = KA + (NT * QB + 1) / 2; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
+      fetch_valid(tf, fslot);
+    }
   };
 
   // ---- interval-2 publication: A(t)'s partial S^T and the tile's key norms ---------------
@@ -605,14 +633,13 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
   };
 
-  // t = 0: A only, then the last tile of the ring's first round; the query norms and
-  // A(0)'s publication.
+  // t = 0: A only (with the whole fetch of the last tile of the ring's first round);
+  // the query norms, A(0)'s publication and tile 0's mixing operands.
   load_v(0, vv);
   // The query rows share slot R-1 with the tile fetched next; their reads into qf
   // are complete (the norms above consumed them).
   wait_lds_reads();
-  if (R - 1 < nkt) stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, std::true_type{});
-  else stage_a(0, IC<0>{}, 0, IC<R - 1>{}, std::false_type{});
+  stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KDMA>{});
   lds_barrier();
   if (tid < BM) {
     float ss = 0.f;
@@ -622,23 +649,30 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     sm.rq[tid] = ss < 0.f ? 0.f : (ss > eps2 ? __builtin_amdgcn_rsqf(ss) : inv_eps);
   }
   publish();
+  if constexpr (SPLIT) stage_t(IC<0>{});
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
-  // t reads tile t-1's mixing operands, runs B(t-1), then A(t) while refilling
-  // tile t-1's slot with ring tile t+R-1 (a key tile, or past the last one the gate
-  // rows); then C(t-1) and A(t)'s publication.
+  // t runs B(t-1), then A(t); then C(t-1) and A(t)'s publication, and refills tile
+  // t-1's slot with tile t+R-1. With SPLIT, T(t) (tile t's mixing operands) closes
+  // the iteration, so tile t-1's slot is free all along and its refill spreads over
+  // A(t) and C(t-1); otherwise T(t-1) opens it and the refill waits for its reads.
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
-    stage_t(IC<PREV>{});
-    // B first: the V words it consumes were loaded before this iteration's DMAs, so
-    // waiting for them (vmcnt counts in issue order) never waits for the refill.
+    const bool refill = t + R - 1 < nkt;
+    if constexpr (!SPLIT) stage_t(IC<PREV>{});
+    // The V words B consumes were loaded an iteration ago.
     stage_b(t - 1);
-    wait_lds_reads();  // the refill below overwrites what stage_t read
-    if (t + R - 1 < nkt) stage_a(t, cur, t + R - 1, IC<PREV>{}, std::true_type{});
-    else stage_a(t, cur, 0, IC<PREV>{}, std::false_type{});
+    if constexpr (!SPLIT) wait_lds_reads();  // the refill overwrites what T read
+    stage_a(t, cur, t + R - 1, IC<PREV>{}, refill, IC<KA>{});
     lds_barrier();
-    stage_c();
+    stage_c(t + R - 1, IC<PREV>{}, refill);
     publish();
+    if constexpr (SPLIT) {
+      // T(t) overwrites the operands C just used: keep the scheduler from hoisting
+      // its reads above C's MFMAs (two live copies would not fit the registers).
+      __builtin_amdgcn_sched_barrier(0);
+      stage_t(cur);
+    }
     lds_barrier();
   };
   int t = 1;
@@ -657,19 +691,21 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if (t < nkt) iteration(t, IC<1>{});
     if (t + 1 < nkt) iteration(t + 1, IC<2>{});
   }
-  // Tail: the last tile's mixing operands; every slot is then free, and the gate rows
-  // (already in the L2) stream into this wave's part of slots 0 / 1 while the last
-  // reduction and mixing product run.
-  switch ((nkt - 1) % R) {
-    case 0: stage_t(IC<0>{}); break;
-    case 1: stage_t(IC<1>{}); break;
-    default: stage_t(IC<(R == 3 ? 2 : 0)>{}); break;
+  // Tail: the last tile's mixing operands (SPLIT: already in registers); every slot
+  // is then free, so the gate rows (already in the L2) stream into this wave's part
+  // of slots 0 / 1 while the last reduction and mixing product run.
+  if constexpr (!SPLIT) {
+    switch ((nkt - 1) % R) {
+      case 0: stage_t(IC<0>{}); break;
+      case 1: stage_t(IC<1>{}); break;
+      default: stage_t(IC<(R == 3 ? 2 : 0)>{}); break;
+    }
+    wait_lds_reads();
   }
-  wait_lds_reads();
   if (has_gate) fetch_rows(gb, erows_base);
   stage_b(nkt - 1);
   lds_barrier();
-  stage_c();
+  stage_c(0, IC<0>{}, false);
 
   // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
   uint32_t a3[G / 2];
