@@ -453,14 +453,21 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   if constexpr (R == 3) {
     if (1 < nkt) fetch_keys(1, IC<1>{});
   }
-  // The gate rows are first read at the end; one touch per 128-byte line now brings
-  // them into the L2, so that their fetch in the tail does not wait on HBM.
-  if (has_gate) {
+  // The gate rows are first read in the tail; one touch per 128-byte line ahead of
+  // that brings them into the L2, so that their fetch does not wait on HBM. When the
+  // whole grid's gate rows fit the L2s with room to spare (8 MB over 8 XCDs) the
+  // touch goes out now; otherwise three key tiles before the tail, as touching them
+  // all at once would push the key tiles out of the L2.
+  constexpr int kTouchLead = 3;
+  const bool gate_fits = (uint64_t)B * (uint64_t)C * row_bytes <= (8ull << 20);
+  const int touch_t = gate_fits ? 0 : nkt - kTouchLead;  // the iteration that touches; < 1: here
+  auto touch_gate = [&]() {
     const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), row_bytes);
     constexpr int kTouches = (BM * 4 * 32 * NK * 2 / 128 + kThreads - 1) / kThreads;  // lines over 256 lanes
 #pragma unroll
     for (int i = 0; i < kTouches; ++i) dma4(r, touch_sink, (uint32_t)(i * kThreads + tid) * 128u);
-  }
+  };
+  if (has_gate && touch_t < 1) touch_gate();
   uint32_t qv[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
@@ -662,6 +669,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if constexpr (!SPLIT) stage_t(IC<PREV>{});
     // The V words B consumes were loaded an iteration ago.
     stage_b(t - 1);
+    if (has_gate && t == touch_t) touch_gate();
     if constexpr (!SPLIT) wait_lds_reads();  // the refill overwrites what T read
     stage_a(t, cur, t + R - 1, IC<PREV>{}, refill, IC<KA>{});
     lds_barrier();
