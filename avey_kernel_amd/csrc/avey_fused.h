@@ -711,18 +711,8 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     wait_lds_reads();
   }
   if (has_gate) fetch_rows(gb, erows_base);
-  stage_b(nkt - 1);
-  lds_barrier();
-  stage_c(0, IC<0>{}, false);
-
-  // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
-  uint32_t a3[G / 2];
-#pragma unroll
-  for (int m = 0; m < G / 2; ++m)
-    a3[m] = 16u * (uint32_t)(li * CPRP + swzc<G>(li, 2 * m + (lg >> 1))) + 8u * (uint32_t)(lg & 1);
-  auto efrag = [&](int qb, int t2) -> char* {
-    return erows_base(qb >> 1) + a3[t2 % (G / 2)] + 16 * (16 * (qb & 1) * CPRP + G * (t2 / (G / 2)));
-  };
+  // The epilogue's bias words and validity bytes, now that the query fragments are
+  // dead: their latency hides behind the last reduction and mixing product.
   u32x2 bw[NT];
   uint32_t qv2[QB];
   {
@@ -735,6 +725,18 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
   }
+  stage_b(nkt - 1);
+  lds_barrier();
+  stage_c(0, IC<0>{}, false);
+
+  // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
+  uint32_t a3[G / 2];
+#pragma unroll
+  for (int m = 0; m < G / 2; ++m)
+    a3[m] = 16u * (uint32_t)(li * CPRP + swzc<G>(li, 2 * m + (lg >> 1))) + 8u * (uint32_t)(lg & 1);
+  auto efrag = [&](int qb, int t2) -> char* {
+    return erows_base(qb >> 1) + a3[t2 % (G / 2)] + 16 * (16 * (qb & 1) * CPRP + G * (t2 / (G / 2)));
+  };
   float rden[QB];
   if (p.normalize) {
 #pragma unroll
