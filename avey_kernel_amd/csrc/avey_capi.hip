@@ -80,7 +80,8 @@ bool device_ok(int dev) {
 //   * slice width DS = 32 * ceil(D / 128) features per wave (4 waves cover D);
 //   * BM = 64 query rows while the double-buffered key slices and the partial
 //     similarity tiles fit the 160 KB of LDS (DS <= 192), else 32;
-//   * BM halves (down to 16) while the grid would leave CUs of the 256 idle.
+//   * BM halves (down to 16) while the grid would leave CUs of the 256 idle;
+//   * the 16-row variants run 8 waves (warp-specialized), the others 4.
 // The fused kernel addresses memory with 16-byte row chunks and 32-bit buffer
 // offsets, so it also needs D % 8 == 0, 16-byte aligned z_tr / z_tl / out, an
 // 8-byte aligned bias, at most 2^30 elements per batch item and C <= 32768 (V
@@ -97,10 +98,11 @@ Plan make_plan(const avey_fwd_args& a) {
     pl.kernel = 1;
     pl.bn = 32;
     pl.bd = 32 * nk;
-    pl.threads = 256;
     int bm = nk <= 6 ? 64 : 32;
     while (bm > 16 && cdiv(a.context, bm) * a.batch < 256) bm /= 2;
     pl.bm = bm;
+    // The 16-row variants are warp-specialized: 4 product waves and 4 helper waves.
+    pl.threads = bm == 16 ? 512 : 256;
     const int64_t nqt = cdiv(a.context, bm);
     pl.grid = nqt * a.batch;
     pl.work_bytes = 0;
@@ -169,7 +171,7 @@ int avey_fwd_plan(const avey_fwd_args* args, avey_fwd_plan_t* out) {
   out->block_n = pl.bn;
   out->block_d = pl.bd;
   out->threads = pl.threads;
-  out->waves_per_simd = 1;
+  out->waves_per_simd = pl.threads / 256;
   out->grid = pl.grid;
   out->workspace_bytes = pl.work_bytes;
   out->key_tile_steps = pl.key_tile_steps;

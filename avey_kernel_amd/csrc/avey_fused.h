@@ -27,6 +27,12 @@
 // partials; the staged key rows are double-buffered (C(t-1) reads one buffer
 // while A(t) fills the other).
 //
+// The 16-row variants run 8 waves instead: waves 0-3 do A, C and the staging as
+// above, waves 4-7 ("helpers", one per feature slice) do B, the V loads, the key
+// norm reciprocals and the key-tile refills, in a program of their own that passes
+// the same barriers. Each SIMD then holds a product wave and a helper wave, and
+// the reduction and the memory traffic no longer stall the MFMAs.
+//
 // The epilogue multiplies by 1 / (den + eps), adds bias, applies the activation,
 // multiplies by the gate, zeroes padded rows and rounds once (ops.py:79-91).
 //
@@ -229,6 +235,13 @@ struct Geo {
   static constexpr int R = 3 * TILE + OVF + SMALL <= kLdsMax ? 3 : 2;
   static_assert(2 * TILE + OVF + SMALL <= kLdsMax, "tile does not fit the LDS");
   static_assert(BM <= 32 * R, "query rows must fit the ring");
+  // Warp specialization (16-row variants, whose waves fit 256 registers): 8 waves,
+  // waves 0-3 run the products on their feature slices as in the 4-wave kernel,
+  // waves 4-7 ("helpers", helper h for slice h) run the reduction, the V loads, the
+  // key reciprocals and the refill DMAs, so that none of these stalls the MFMAs, and
+  // each SIMD holds two waves whose stalls the other fills.
+  static constexpr bool WS = BM == 16;
+  static constexpr int THREADS = (WS ? 2 : 1) * kThreads;
 };
 
 template <int G>
@@ -277,8 +290,9 @@ __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0x
 // Otherwise chunks at or past D are redirected to kNowhere (D % 8 == 0 makes a
 // chunk wholly in or out).
 template <typename T16, int BM, int NK, bool FULL>
-__global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(FwdParams p) {
   typedef Geo<BM, NK> Gm;
+  constexpr bool WS = Gm::WS;
   constexpr int QB = Gm::QB, DS = Gm::DS, NT = Gm::NT, CPR = Gm::CPR, CPRP = Gm::CPRP, G = Gm::G;
   constexpr int SLICE = Gm::SLICE, TILE = Gm::TILE, R = Gm::R, KDMA = Gm::KDMA;
   constexpr int UNITS = 2 * QB, UPW = (UNITS + kWaves - 1) / kWaves;
@@ -297,8 +311,13 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 
   // The wave index is read into a scalar register, so that LDS addresses built
   // from it (DMA destinations go through M0) stay scalar.
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
+  // w: the feature slice this wave serves; helper: a warp-specialized helper wave
+  // (helpers branch off into a loop of their own before the first key tile).
+  const int w = WS ? (wv & (kWaves - 1)) : wv;
+  const bool helper = WS && wv >= kWaves;
+  const bool do_mma = !helper;
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
   const int n_qt = (C + BM - 1) / BM;
   const int b = (int)blockIdx.x % B;
@@ -404,13 +423,18 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
   };
   // DMA instruction j (of KDMA) of key tile t into this wave's part of a ring slot.
+  // The refills sit under uniform branches (`if (refill)`), not issued through an
+  // empty resource when there is nothing to fetch: unconditional copies into a
+  // free slot have been seen to make the compiler drop the wait that a later read
+  // of the other slot needs (it read a tile whose copies were still in flight).
   auto fetch_key_part = [&](int t, char* dst, int j, const uint32_t (&kof)[P]) {
     dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, row_bytes), dst + 1024 * j, kof[j % P]);
   };
-  auto fetch_valid = [&](int t, auto slot) {
+  auto fetch_valid = [&](int t, auto slot, bool live = true) {
     constexpr int I = decltype(slot)::value;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, valid_rows, 1u), (uint32_t)li);
+    for (int kb = 0; kb < 2; ++kb)
+      zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, live ? valid_rows : 0, 1u), (uint32_t)li);
   };
   auto fetch_keys = [&](int t, auto slot) {
     uint32_t kof[P];
@@ -448,10 +472,12 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   };
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
-  fetch_rows((const char*)zb, qrows_base);
-  fetch_keys(0, IC<0>{});
-  if constexpr (R == 3) {
-    if (1 < nkt) fetch_keys(1, IC<1>{});
+  if (do_mma) {
+    fetch_rows((const char*)zb, qrows_base);
+    fetch_keys(0, IC<0>{});
+    if constexpr (R == 3) {
+      if (1 < nkt) fetch_keys(1, IC<1>{});
+    }
   }
   // The gate rows are first read in the tail; one touch per 128-byte line ahead of
   // that brings them into the L2, so that their fetch does not wait on HBM. When the
@@ -461,17 +487,18 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   constexpr int kTouchLead = 3;
   const bool gate_fits = (uint64_t)B * (uint64_t)C * row_bytes <= (8ull << 20);
   const int touch_t = gate_fits ? 0 : nkt - kTouchLead;  // the iteration that touches; < 1: here
-  auto touch_gate = [&]() {
+  auto touch_gate = [&]() {  // by the 256 lanes of the product waves
     const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), row_bytes);
     constexpr int kTouches = (BM * 4 * 32 * NK * 2 / 128 + kThreads - 1) / kThreads;  // lines over 256 lanes
 #pragma unroll
     for (int i = 0; i < kTouches; ++i) dma4(r, touch_sink, (uint32_t)(i * kThreads + tid) * 128u);
   };
-  if (has_gate && touch_t < 1) touch_gate();
+  if (do_mma && has_gate && touch_t < 1) touch_gate();
+  u32x4 qf[QB][NK];
+  if (do_mma) {
   uint32_t qv[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
-  u32x4 qf[QB][NK];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const bool ok = (16 * qb + li < C - q0) && ((qv[qb] | or_valid) != 0u);
@@ -484,6 +511,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
     ss = sum_over_groups(ss);
     if (lg == 0) sm.nq[w][16 * qb + li] = ok ? ss : -1.f;
+  }
   }
 
   f32x4 oacc[NT][QB];
@@ -601,10 +629,11 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 
   // ---- C: mixing of the previous tile from the transposed operands in registers; with
   // FETCH, the second part of the refill A started (one DMA every other MFMA) ------------
-  auto stage_c = [&](int tf, auto fslot, bool refill) {
-    if constexpr (!SPLIT) refill = false;
+  // FETCH: this variant issues (part of) the refill here; `refill`: it is a real one.
+  auto stage_c = [&](int tf, auto fslot, bool refill, auto fetch) {
+    constexpr bool FETCH = SPLIT && decltype(fetch)::value;
     uint32_t kof[P];
-    if constexpr (SPLIT) key_offsets(kof);
+    if constexpr (FETCH) key_offsets(kof);
     u32x4 pf[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) pf[qb] = px[qb][lane];
@@ -614,24 +643,26 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
       for (int qb = 0; qb < QB; ++qb) {
         oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pf[qb], oacc[t2][qb]);
         const int m = t2 * QB + qb;
-        if (m % 2 == 0 && KA + m / 2 < KDMA && refill) fetch_key_part(tf, slot_base(fslot), KA + m / 2, kof);
+        if (m % 2 == 0 && KA + m / 2 < KDMA && FETCH && refill) fetch_key_part(tf, slot_base(fslot), KA + m / 2, kof);
       }
-    if (refill) {
+    if (FETCH && refill) {
 #pragma unroll
       for (int j = KA + (NT * QB + 1) / 2; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
       fetch_valid(tf, fslot);
     }
   };
 
-  // ---- interval-2 publication: A(t)'s partial S^T and the tile's key norms ---------------
-  auto publish = [&]() {
+  // ---- interval-2 publication: A(t)'s partial S^T (product waves) and the tile's key
+  // reciprocals (reduction waves: every one computes the same values, lanes 32..63
+  // repeating 0..31, so no wave waits on a branch here) ---------------------------------
+  auto publish = [&](auto mma, auto red) {
+    if constexpr (decltype(mma)::value) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sx[w][kb][qb][lane] = sacc[kb][qb];
-    // Every wave computes the same key reciprocals (lanes 32..63 repeat 0..31), so
-    // no wave waits on a branch here.
-    {
+        for (int qb = 0; qb < QB; ++qb) sx[w][kb][qb][lane] = sacc[kb][qb];
+    }
+    if constexpr (decltype(red)::value) {
       const int k = lane & (kBN - 1);
       const float n = (sm.nxp[0][k] + sm.nxp[1][k]) + (sm.nxp[2][k] + sm.nxp[3][k]);
       // A float store: an element assignment to the vector would be a read-modify-
@@ -640,13 +671,90 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
   };
 
+  // ---- warp-specialized refill: a helper fetches key tile tf into its slice of slot F
+  // as its last memory instructions of the iteration and has it land before the
+  // iteration's closing barrier. The product waves cannot wait for another wave's
+  // copies, so this wait and the barrier are what orders their reads after the copy.
+  // (Leaving the refill in flight for one more iteration where the ring has three
+  // slots measured no faster: the wait is off the critical path.) -----------------
+  auto refill_all = [&](int tf, auto fslot) {
+    uint32_t kof[P];
+    key_offsets(kof);
+#pragma unroll
+    for (int j = 0; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
+  };
+  // s_waitcnt vmcnt(0) (gfx9 encoding; expcnt and lgkmcnt at their maxima, i.e. not
+  // waited for).
+  auto wait_refill = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };
+
   // t = 0: A only (with the whole fetch of the last tile of the ring's first round);
-  // the query norms, A(0)'s publication and tile 0's mixing operands.
-  load_v(0, vv);
-  // The query rows share slot R-1 with the tile fetched next; their reads into qf
-  // are complete (the norms above consumed them).
+  // the query norms, A(0)'s publication and tile 0's mixing operands. The query rows
+  // share slot R-1 with that tile; their reads into qf are complete (the norms above
+  // consumed them) before the refill is issued (after the barrier, by a helper).
+  // Steady-state iterations run over t = 1 .. nkt-1, unrolled by R so that every slot
+  // index is a constant.
+  auto run_loop = [&](auto iter) {
+    int t = 1;
+    if constexpr (R == 2) {
+      for (; t + 1 < nkt; t += 2) {
+        iter(t, IC<1>{});
+        iter(t + 1, IC<0>{});
+      }
+      if (t < nkt) iter(t, IC<1>{});
+    } else {
+      for (; t + 2 < nkt; t += 3) {
+        iter(t, IC<1>{});
+        iter(t + 1, IC<2>{});
+        iter(t + 2, IC<0>{});
+      }
+      if (t < nkt) iter(t, IC<1>{});
+      if (t + 1 < nkt) iter(t + 1, IC<2>{});
+    }
+  };
+  using TT = std::true_type;
+  using FF = std::false_type;
+  if constexpr (WS) {
+    if (helper) {
+      // The helpers' program: the same barriers as the product waves', in order.
+      load_v(0, vv);
+      lds_barrier();  // A(0) done, the query rows in slot R-1 consumed
+      if (R - 1 < nkt) refill_all(R - 1, IC<R - 1>{});
+      publish(FF{}, TT{});
+      wait_refill();
+      lds_barrier();
+      run_loop([&](int t, auto cur) {
+        constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
+        const bool refill = t + R - 1 < nkt;
+        // The V words B consumes were loaded an iteration ago; the refill goes last.
+        stage_b(t - 1);
+        if (refill) refill_all(t + R - 1, IC<PREV>{});
+        lds_barrier();
+        publish(FF{}, TT{});
+        wait_refill();
+        lds_barrier();
+      });
+      stage_b(nkt - 1);
+      lds_barrier();
+      if (p.normalize) {
+#pragma unroll
+        for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
+        lds_barrier();
+        lds_barrier();
+      }
+      return;
+    }
+  }
+  // From here on: the product waves (all waves without warp specialization).
+  constexpr bool RED = !WS;
+  using RT = std::integral_constant<bool, RED>;
+  if constexpr (RED) load_v(0, vv);
   wait_lds_reads();
-  stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KDMA>{});
+  if constexpr (WS) {
+    fetch_valid(R - 1, IC<R - 1>{}, R - 1 < nkt);
+    stage_a(0, IC<0>{}, 0, IC<R - 1>{}, false, IC<0>{});
+  } else {
+    stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KDMA>{});
+  }
   lds_barrier();
   if (tid < BM) {
     float ss = 0.f;
@@ -655,7 +763,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     // F.normalize divides by max(||q||, norm_eps); 0 marks padded / out-of-range rows.
     sm.rq[tid] = ss < 0.f ? 0.f : (ss > eps2 ? __builtin_amdgcn_rsqf(ss) : inv_eps);
   }
-  publish();
+  publish(TT{}, RT{});
   if constexpr (SPLIT) stage_t(IC<0>{});
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
@@ -666,6 +774,20 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     const bool refill = t + R - 1 < nkt;
+    if constexpr (WS) {
+      static_assert(!WS || SPLIT, "warp specialization keeps T at the end of the iteration");
+      // The helpers run B and the refill meanwhile (see their program above).
+      if (has_gate && t == touch_t) touch_gate();
+      fetch_valid(t + R - 1, IC<PREV>{}, refill);
+      stage_a(t, cur, 0, IC<PREV>{}, false, IC<0>{});
+      lds_barrier();
+      stage_c(0, IC<PREV>{}, false, FF{});
+      publish(TT{}, FF{});
+      __builtin_amdgcn_sched_barrier(0);
+      stage_t(cur);
+      lds_barrier();
+      return;
+    }
     if constexpr (!SPLIT) stage_t(IC<PREV>{});
     // The V words B consumes were loaded an iteration ago.
     stage_b(t - 1);
@@ -673,8 +795,8 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     if constexpr (!SPLIT) wait_lds_reads();  // the refill overwrites what T read
     stage_a(t, cur, t + R - 1, IC<PREV>{}, refill, IC<KA>{});
     lds_barrier();
-    stage_c(t + R - 1, IC<PREV>{}, refill);
-    publish();
+    stage_c(t + R - 1, IC<PREV>{}, refill, TT{});
+    publish(TT{}, TT{});
     if constexpr (SPLIT) {
       // T(t) overwrites the operands C just used: keep the scheduler from hoisting
       // its reads above C's MFMAs (two live copies would not fit the registers).
@@ -683,22 +805,7 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
     }
     lds_barrier();
   };
-  int t = 1;
-  if constexpr (R == 2) {
-    for (; t + 1 < nkt; t += 2) {
-      iteration(t, IC<1>{});
-      iteration(t + 1, IC<0>{});
-    }
-    if (t < nkt) iteration(t, IC<1>{});
-  } else {
-    for (; t + 2 < nkt; t += 3) {
-      iteration(t, IC<1>{});
-      iteration(t + 1, IC<2>{});
-      iteration(t + 2, IC<0>{});
-    }
-    if (t < nkt) iteration(t, IC<1>{});
-    if (t + 1 < nkt) iteration(t + 1, IC<2>{});
-  }
+  run_loop(iteration);
   // Tail: the last tile's mixing operands (SPLIT: already in registers); every slot
   // is then free, so the gate rows (already in the L2) stream into this wave's part
   // of slots 0 / 1 while the last reduction and mixing product run.
@@ -725,9 +832,9 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
   }
-  stage_b(nkt - 1);
+  if constexpr (RED) stage_b(nkt - 1);
   lds_barrier();
-  stage_c(0, IC<0>{}, false);
+  stage_c(0, IC<0>{}, false, FF{});
 
   // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
   uint32_t a3[G / 2];
@@ -739,8 +846,10 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   };
   float rden[QB];
   if (p.normalize) {
+    if constexpr (RED) {
 #pragma unroll
-    for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
+      for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
+    }
     lds_barrier();
     if (tid < BM) {
       float d = 0.f;
@@ -763,6 +872,12 @@ __global__ __launch_bounds__(kThreads, 1) void fused_fwd_kernel(FwdParams p) {
   // compiler cannot tell the reads from the writes apart, and interleaved they
   // would pay one LDS round trip each.
   constexpr int GB = NT <= 12 ? NT : 8;
+  // The gate rows' DMAs must have landed before the reads below. The compiler's
+  // LDS-DMA wait tracking has been seen to drop this wait (the 8-wave variant read
+  // gate words still in flight), so it is explicit, and a compiler memory barrier
+  // keeps the reads after it; the bias and validity loads it also drains are
+  // consumed right away.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   auto finish = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
@@ -820,9 +935,9 @@ hipError_t launch_fused_bm(const FwdParams& p, int nk, int64_t grid, hipStream_t
 template <typename T16, int BM, int NK>
 hipError_t launch_fused_one(const FwdParams& p, int64_t grid, hipStream_t s) {
   if (p.D == 4 * 32 * NK)
-    fused_fwd_kernel<T16, BM, NK, true><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(p);
+    fused_fwd_kernel<T16, BM, NK, true><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
   else
-    fused_fwd_kernel<T16, BM, NK, false><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(p);
+    fused_fwd_kernel<T16, BM, NK, false><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
   return hipGetLastError();
 }
 

@@ -1,0 +1,255 @@
+"""Static check of the buffer-to-LDS copy waits in the fused kernel's gfx950 code.
+
+The fused kernel stages key tiles, query rows and gate rows in LDS with
+``buffer_load_dwordx4 ... lds`` (one instruction copies 64 lanes x 16 bytes). A
+wave must execute ``s_waitcnt vmcnt(N)`` before it reads those rows, with N small
+enough that the copy has retired. The compiler derives these waits from its own
+tracking of which LDS object a copy writes, and that tracking has been seen to
+drop a wait: a read of a ring slot whose refill was still in flight. Such a read
+fails only when the copy is slow, so the parity tests catch it now and then at
+best; this check finds it in the assembly.
+
+Method: a dataflow over the control-flow graph of each kernel. For every copy
+that may still be in flight at an LDS read it keeps the Pareto set, over paths,
+of (vector-memory loads issued since, barriers passed since); a wait
+``vmcnt(N)`` retires the copies with at least N loads after them (vector memory
+returns in issue order). Reads are classified by the use of their result: key
+operands (16-byte read feeding an MFMA A operand), query operands (B operand),
+mixing operands (``ds_read_b64_tr_b16``) and the epilogue's gate words
+(``ds_read_b64``). The rules, for a ring of R key slots:
+
+* prologue copies (query rows, key tiles 0 .. R-2): before the first barrier no
+  query-row copy may be in flight at a query read, and no query-row or tile-0
+  copy at a key read; after it, no prologue copy at any key or mixing read;
+* ring refills: a copy in flight at a key read has passed at most 2 (R - 2)
+  barriers (an older one filled the slot being read); at a mixing read at most
+  2 (R - 2) + 1 for the 16/32-row variants (they read the mixing operands at the
+  end of the tile's own iteration) or 2 (R - 1) for the 64-row variants (at the
+  start of the next);
+* gate reads: nothing in flight but the 4-byte cache-line touches, whose
+  landing place is never read.
+
+Branch correlations are ignored (every path through the graph counts), so the
+check can over-report but not miss a path. The 8-wave variants' helper waves
+refill slots for the product waves; those copies are ordered by the helpers'
+explicit wait and a barrier, which no single wave's counter shows, and are
+outside this check.
+"""
+
+import re
+from collections import defaultdict
+
+CAP_LOADS, CAP_BARRIERS = 64, 9
+_KERNEL = re.compile(r'^(_ZN4avey16fused_fwd_kernelI\w+):', re.M)
+_SHAPE = re.compile(r'fused_fwd_kernelI\w+?Li(\d+)ELi(\d+)ELb(\d)E')
+
+
+def ring(bm, nk):
+    """(R, copies per key tile, copies for the query rows) of a (BM, NK) variant,
+    as the kernel's LDS geometry fixes them."""
+    cpr = 4 * nk
+    cprp = (cpr + 7) // 8 * 8
+    tile = 4 * 32 * cprp * 16
+    qb = bm // 16
+    sx, px = 4 * 2 * qb * 64 * 16, (qb + 1) * 64 * 16
+    ovf = tile if (bm > 32 and tile > sx + px) else sx + px
+    small = 4 * (4 * 32 + 32 + 4 * bm + bm + (qb + 1) * 2 * 4 * 16 + bm)
+    r = 3 if 3 * tile + ovf + small <= 160 * 1024 else 2
+    return r, 32 * cprp // 64, bm * cprp // 64
+
+
+def kernels(asm_text):
+    """{symbol: [instruction or 'label:' strings]} for each fused kernel."""
+    out = {}
+    for m in _KERNEL.finditer(asm_text):
+        name = m.group(1)
+        body = asm_text[m.end():asm_text.index('.Lfunc_end', m.end())]
+        lines = []
+        for raw in body.split('\n'):
+            t = ' '.join(raw.split(';')[0].split())
+            if not t or (t.startswith('.') and not t.startswith('.LBB')):
+                continue
+            lines.append(t)
+        out[name] = lines
+    return out
+
+
+def _blocks(lines):
+    blocks, cur, anon = [], ['entry', []], 0
+    for t in lines:
+        if t.endswith(':'):
+            blocks.append(cur)
+            cur = [t[:-1], []]
+            continue
+        cur[1].append(t)
+        if t.split()[0].startswith(('s_branch', 's_cbranch', 's_endpgm', 's_setpc')):
+            blocks.append(cur)
+            anon += 1
+            cur = [f'<fallthrough {anon}>', []]
+    blocks.append(cur)
+    index = {b[0]: k for k, b in enumerate(blocks)}
+    succ = []
+    for k, (_, ins) in enumerate(blocks):
+        op = ins[-1].split() if ins else ['']
+        nxt = [k + 1] if k + 1 < len(blocks) else []
+        if op[0] == 's_branch':
+            succ.append([index[op[1]]])
+        elif op[0].startswith('s_cbranch'):
+            succ.append([index[op[1]]] + nxt)
+        elif op[0] in ('s_endpgm', 's_setpc_b64'):
+            succ.append([])
+        else:
+            succ.append(nxt)
+    return blocks, succ
+
+
+def _is_vmem_load(t):
+    return t.startswith(('buffer_load', 'global_load', 'flat_load'))
+
+
+def _is_copy(t):
+    return _is_vmem_load(t) and t.endswith(' lds')
+
+
+def _is_touch(t):
+    return t.startswith('buffer_load_dword ') and t.endswith(' lds')
+
+
+def _add(front, pair):
+    loads, bars = pair
+    if any(l2 <= loads and b2 >= bars for l2, b2 in front):
+        return front, False
+    return [p for p in front if not (loads <= p[0] and bars >= p[1])] + [pair], True
+
+
+def _regs(tok):
+    m = re.match(r'([va])\[(\d+):(\d+)\]$', tok)
+    if m:
+        return m.group(1), int(m.group(2)), int(m.group(3))
+    m = re.match(r'([va])(\d+)$', tok)
+    return (m.group(1), int(m.group(2)), int(m.group(2))) if m else None
+
+
+def _role(flat, i):
+    """'T' mixing, 'G' gate, 'A' key operand, 'Q' query operand, or None."""
+    t = flat[i]
+    if t.startswith('ds_read_b64_tr'):
+        return 'T'
+    if t.startswith('ds_read_b64 '):
+        return 'G'
+    if not t.startswith('ds_read_b128'):
+        return None
+    dst = _regs(t.split()[1].rstrip(','))
+    if dst is None:
+        return None
+    for t2 in flat[i + 1:i + 600]:
+        parts = [x.rstrip(',') for x in t2.split()]
+        if parts[0].startswith('v_mfma') and len(parts) >= 4:
+            for pos, tok in enumerate(parts[2:4]):
+                r = _regs(tok)
+                if r and r[0] == dst[0] and r[1] <= dst[1] and dst[2] <= r[2]:
+                    return 'A' if pos == 0 else 'Q'
+        if len(parts) > 1 and not parts[0].startswith(('ds_write', 'buffer_store', 'v_cmp', 's_')):
+            r = _regs(parts[1])
+            if r and r[0] == dst[0] and not (r[2] < dst[1] or r[1] > dst[2]):
+                return None  # overwritten before any MFMA used it
+    return None
+
+
+def check_kernel(lines, bm, nk):
+    """Violations [(read, rule)] and per-role read counts of one kernel."""
+    r, kdma, nq = ring(bm, nk)
+    split = bm <= 32
+    blocks, succ = _blocks(lines)
+    order, gidx, flat, first_barrier = [], {}, [], None
+    for k, (_, ins) in enumerate(blocks):
+        for p, t in enumerate(ins):
+            gidx[(k, p)] = len(flat)
+            flat.append(t)
+            if _is_copy(t) and not _is_touch(t):
+                order.append((k, p))
+            if t.startswith('s_barrier') and first_barrier is None:
+                first_barrier = len(flat) - 1
+    if first_barrier is None:
+        first_barrier = len(flat)
+    prologue = [s for s in order if gidx[s] < first_barrier]
+    pro_q = set(prologue[:nq])
+    pro_t0 = set(prologue[nq:nq + kdma])
+    pro_all = set(prologue[:nq + (r - 1) * kdma])
+
+    state_in = [None] * len(blocks)
+    state_in[0] = {}
+    work = [0]
+    at_read = {}
+    while work:
+        k = work.pop(0)
+        st = {s: list(f) for s, f in state_in[k].items()}
+        for p, t in enumerate(blocks[k][1]):
+            m = re.search(r'vmcnt\((\d+)\)', t) if t.startswith('s_waitcnt') else None
+            if m:
+                n = int(m.group(1))
+                st = {s: [q for q in f if q[0] < n] for s, f in st.items()}
+                st = {s: f for s, f in st.items() if f}
+            elif t.startswith('s_barrier'):
+                st = {s: [(q[0], min(q[1] + 1, CAP_BARRIERS)) for q in f] for s, f in st.items()}
+            elif _is_vmem_load(t):
+                st = {s: [(min(q[0] + 1, CAP_LOADS), q[1]) for q in f] for s, f in st.items()}
+                if _is_copy(t) and not _is_touch(t):
+                    st[(k, p)] = [(0, 0)]
+            elif t.startswith('ds_read'):
+                at_read[(k, p)] = st
+        for s2 in succ[k]:
+            if state_in[s2] is None:
+                state_in[s2] = {s: list(f) for s, f in st.items()}
+                work.append(s2)
+                continue
+            new, changed = {s: list(f) for s, f in state_in[s2].items()}, False
+            for s, f in st.items():
+                front = new.get(s, [])
+                for q in f:
+                    front, c = _add(front, q)
+                    changed |= c
+                new[s] = front
+            if changed:
+                state_in[s2] = new
+                work.append(s2)
+
+    lim_key = 2 * (r - 2)
+    lim_mix = 2 * (r - 2) + 1 if split else 2 * (r - 1)
+    counts, bad = defaultdict(int), []
+    for (k, p), st in at_read.items():
+        i = gidx[(k, p)]
+        role = _role(flat, i)
+        if role is None:
+            continue
+        counts[role] += 1
+        for s, front in st.items():
+            bars = max(q[1] for q in front)
+            why = None
+            if role == 'G':
+                why = 'gate read with a copy in flight'
+            elif i < first_barrier:
+                if role == 'Q' and s in pro_q:
+                    why = 'query read with a query-row copy in flight'
+                elif role == 'A' and (s in pro_q or s in pro_t0):
+                    why = 'tile-0 key read with a prologue copy in flight'
+            elif role in ('A', 'T') and s in pro_all:
+                why = 'prologue copy in flight after the first barrier'
+            elif role == 'A' and bars > lim_key:
+                why = f'key read with a copy {bars} barriers old in flight (at most {lim_key})'
+            elif role == 'T' and bars > lim_mix:
+                why = f'mixing read with a copy {bars} barriers old in flight (at most {lim_mix})'
+            if why:
+                bad.append((f'{blocks[k][0]}+{p}: {flat[i]}', f'{why}; copy at {blocks[s[0]][0]}+{s[1]}'))
+    return bad, dict(counts)
+
+
+def check_asm(asm_text):
+    """{kernel: (violations, read counts, (BM, NK))} for every fused kernel in a file."""
+    out = {}
+    for name, lines in kernels(asm_text).items():
+        m = _SHAPE.search(name)
+        bm, nk = int(m.group(1)), int(m.group(2))
+        bad, counts = check_kernel(lines, bm, nk)
+        out[name] = (bad, counts, (bm, nk))
+    return out

@@ -1,0 +1,111 @@
+"""Every LDS read of copied rows in the fused kernel waits for its copy.
+
+The fused sources are compiled to gfx950 assembly with the library's own flags
+and checked by tests/dma_waits.py (its docstring states the rules). The first
+tests pin the checker itself on small hand-written instruction sequences, so that
+the check over the real kernels cannot pass by classifying nothing.
+"""
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+import dma_waits as dw
+from avey_kernel_amd import _build
+
+KEY = ['ds_read_b128 v[10:13], v2', 'v_mfma_f32_16x16x32_bf16 v[20:23], v[10:13], v[30:33], v[20:23]']
+QUERY = ['ds_read_b128 v[10:13], v2', 'v_mfma_f32_16x16x32_bf16 v[20:23], v[30:33], v[10:13], v[20:23]']
+MIX = ['ds_read_b64_tr_b16 v[10:11], v2']
+GATE = ['ds_read_b64 v[10:11], v2']
+COPY = 'buffer_load_dwordx4 v1, s[0:3], 0 offen lds'
+TOUCH = 'buffer_load_dword v1, s[0:3], 0 offen lds'
+LOAD = 'buffer_load_dwordx2 v[4:5], v1, s[0:3], 0 offen'
+
+
+def _bad(lines, bm=32, nk=8):
+    bad, _ = dw.check_kernel(lines + ['s_endpgm'], bm, nk)
+    return bad
+
+
+def test_ring_geometry():
+    # (R, copies per tile, copies for the query rows): C2's variant keeps three
+    # slots, 768-feature rows in the 32-row variant only two.
+    assert dw.ring(16, 6) == (3, 12, 6)
+    assert dw.ring(32, 6) == (2, 12, 12)
+    assert dw.ring(64, 4) == (3, 8, 16)
+
+
+def test_refill_read_without_wait_is_flagged():
+    # Two slots: the copy issued in the previous iteration filled the slot read now.
+    assert _bad(['s_barrier', COPY, 's_barrier'] + KEY)
+    assert not _bad(['s_barrier', COPY, 's_barrier', 's_waitcnt vmcnt(0)'] + KEY)
+    # Three slots: a copy one iteration old (two barriers) is the next tile's.
+    assert not _bad(['s_barrier', COPY, 's_barrier', 's_barrier'] + KEY, bm=16, nk=2)
+    assert _bad(['s_barrier', COPY] + ['s_barrier'] * 3 + KEY, bm=16, nk=2)
+
+
+def test_vmcnt_retires_in_issue_order():
+    # vmcnt(N) leaves the N newest loads in flight: with two loads after the copy,
+    # vmcnt(2) retires it and vmcnt(3) does not.
+    seq = ['s_barrier', COPY, LOAD, LOAD, 's_barrier']
+    assert not _bad(seq + ['s_waitcnt vmcnt(2)'] + KEY)
+    assert _bad(seq + ['s_waitcnt vmcnt(3)'] + KEY)
+
+
+def test_every_path_counts():
+    # The wait sits on one arm of a branch only: the other arm reaches the read
+    # with the copy in flight.
+    seq = ['s_barrier', COPY, 's_barrier', 's_cbranch_scc1 .LBB0_2', 's_waitcnt vmcnt(0)', '.LBB0_2:']
+    assert _bad(seq + KEY)
+    assert not _bad(seq + ['s_waitcnt vmcnt(0)'] + KEY)
+
+
+def test_prologue_and_gate_rules():
+    bm, nk = 16, 2
+    _, kdma, nq = dw.ring(bm, nk)
+    queries, tile0 = [COPY] * nq, [COPY] * kdma
+    assert _bad(queries + tile0 + QUERY, bm, nk)  # query rows not waited for
+    # Waiting for the query rows only (tile 0 may still land) is enough for them.
+    assert not _bad(queries + tile0 + [f's_waitcnt vmcnt({kdma})'] + QUERY, bm, nk)
+    assert _bad(queries + tile0 + [f's_waitcnt vmcnt({kdma})'] + KEY, bm, nk)
+    assert _bad([COPY] + GATE)
+    assert not _bad([TOUCH] + GATE)  # a touch's landing place is never read
+    assert not _bad([COPY, 's_waitcnt vmcnt(0)'] + GATE)
+
+
+def test_mixing_read_rule():
+    # 32-row variants read tile t's mixing operands at the end of iteration t: its
+    # own refill (one barrier back) may be in flight, the previous one may not.
+    assert not _bad(['s_barrier', COPY, 's_barrier'] + MIX)
+    assert _bad(['s_barrier', COPY, 's_barrier', 's_barrier'] + MIX)
+
+
+def _compile(src, out_dir):
+    out = os.path.join(out_dir, os.path.splitext(src)[0] + '.s')
+    cmd = [_build.hipcc(), *_build.HIP_FLAGS, *_build.EXTRA_FLAGS.get(src, []), '--cuda-device-only', '-S',
+           os.path.join(_build.CSRC, src), '-o', out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out
+
+
+@pytest.mark.skipif(shutil.which('hipcc') is None and not os.path.exists('/opt/rocm/bin/hipcc'),
+                    reason='hipcc not available')
+def test_fused_kernels_wait_for_their_copies(tmp_path):
+    sources = [s for s in _build.SOURCES if s.startswith('avey_fused_bm')]
+    with ThreadPoolExecutor(max_workers=min(6, os.cpu_count() or 1)) as pool:
+        files = list(pool.map(lambda s: _compile(s, str(tmp_path)), sources))
+    checked = 0
+    problems = []
+    for path in files:
+        for name, (bad, counts, (bm, nk)) in dw.check_asm(open(path).read()).items():
+            checked += 1
+            # Non-vacuous: the key, query, mixing and gate reads were all found.
+            for role in ('A', 'Q', 'T', 'G'):
+                assert counts.get(role, 0) > 0, (name, counts)
+            problems += [(name, b) for b in bad[:3]]
+    assert checked >= 6 * 10, checked
+    assert not problems, problems[:6]

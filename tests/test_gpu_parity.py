@@ -188,11 +188,14 @@ def test_avey_b_configs_weighted_variant(tag):
 
 
 def test_bitwise_determinism_full_size():
-    for tag in ('C2', 'C4'):
+    # Repeated calls agree bitwise: the summation orders are fixed, and no read races
+    # its producer (a race shows as an occasional difference, hence many calls).
+    for tag in ('C2', 'C4', 'C5'):
         cfg, inp = _config_case(tag)
-        a = wl.call(cfg, inp)
-        b = wl.call(cfg, inp)
-        assert torch.equal(a, b), tag
+        a = wl.call(cfg, inp).clone()
+        for i in range(24):
+            b = wl.call(cfg, inp)
+            assert torch.equal(a, b), f'{tag} call {i}'
 
 
 def test_causal_rows_blind_to_future_full_size():
