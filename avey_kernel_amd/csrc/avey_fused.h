@@ -493,7 +493,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
 #pragma unroll
     for (int i = 0; i < kTouches; ++i) dma4(r, touch_sink, (uint32_t)(i * kThreads + tid) * 128u);
   };
-  if (do_mma && has_gate && touch_t < 1) touch_gate();
+  if (has_gate && touch_t < 1) touch_gate();
   u32x4 qf[QB][NK];
   if (do_mma) {
   uint32_t qv[QB];
@@ -671,21 +671,28 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
   };
 
-  // ---- warp-specialized refill: a helper fetches key tile tf into its slice of slot F
-  // as its last memory instructions of the iteration and has it land before the
-  // iteration's closing barrier. The product waves cannot wait for another wave's
-  // copies, so this wait and the barrier are what orders their reads after the copy.
-  // (Leaving the refill in flight for one more iteration where the ring has three
-  // slots measured no faster: the wait is off the critical path.) -----------------
-  auto refill_all = [&](int tf, auto fslot) {
+  // ---- warp-specialized refill: a helper copies key tile tf into its slice of slot F,
+  // copies [j0, j1) of KDMA. Issuing them is throttled by the CU's memory pipe (about
+  // 50 cycles per copy with four helpers issuing), so a steady-state iteration splits
+  // them: the first half after the reduction (the product waves run A meanwhile), the
+  // second after the key reciprocals (they run C and T). The product waves cannot
+  // wait for another wave's copies: the helper's wait and the next barrier are what
+  // orders their reads after a copy. With three slots a refill is read two barriers
+  // pairs later, so the wait at an iteration's end retires the previous iteration's
+  // refill and leaves this one in flight; with two slots it retires everything. -----
+  auto refill_part = [&](int tf, auto fslot, auto j0, auto j1) {
     uint32_t kof[P];
     key_offsets(kof);
 #pragma unroll
-    for (int j = 0; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
+    for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
   };
-  // s_waitcnt vmcnt(0) (gfx9 encoding; expcnt and lgkmcnt at their maxima, i.e. not
-  // waited for).
-  auto wait_refill = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };
+  // s_waitcnt encodings (gfx9: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at
+  // their maxima, i.e. not waited for).
+  static_assert(KDMA < 64, "vmcnt holds 6 bits");
+  auto wait_all = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+  // All but the newest KDMA vector-memory operations retired (they return in issue
+  // order): the refill just issued may stay in flight.
+  auto wait_keep_refill = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70 | (KDMA & 15) | ((KDMA >> 4) << 14)); };
 
   // t = 0: A only (with the whole fetch of the last tile of the ring's first round);
   // the query norms, A(0)'s publication and tile 0's mixing operands. The query rows
@@ -716,21 +723,26 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   if constexpr (WS) {
     if (helper) {
       // The helpers' program: the same barriers as the product waves', in order.
+      constexpr int KH = KDMA / 2;
       load_v(0, vv);
       lds_barrier();  // A(0) done, the query rows in slot R-1 consumed
-      if (R - 1 < nkt) refill_all(R - 1, IC<R - 1>{});
+      if (R - 1 < nkt) refill_part(R - 1, IC<R - 1>{}, IC<0>{}, IC<KDMA>{});
       publish(FF{}, TT{});
-      wait_refill();
+      wait_all();
       lds_barrier();
       run_loop([&](int t, auto cur) {
         constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
         const bool refill = t + R - 1 < nkt;
-        // The V words B consumes were loaded an iteration ago; the refill goes last.
+        // The V words B consumes were loaded an iteration ago.
         stage_b(t - 1);
-        if (refill) refill_all(t + R - 1, IC<PREV>{});
+        if (refill) refill_part(t + R - 1, IC<PREV>{}, IC<0>{}, IC<KH>{});
         lds_barrier();
         publish(FF{}, TT{});
-        wait_refill();
+        if (refill) refill_part(t + R - 1, IC<PREV>{}, IC<KH>{}, IC<KDMA>{});
+        if (R == 3 && refill)
+          wait_keep_refill();
+        else
+          wait_all();
         lds_barrier();
       });
       stage_b(nkt - 1);
