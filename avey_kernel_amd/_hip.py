@@ -4,7 +4,10 @@ The op is functional: it allocates and returns a fresh output, as the
 reference's ``avey_kernels::mix`` does (``avey_kernels/_triton.py:153-188``),
 and has a fake implementation so fake-tensor tracing and
 ``torch.compile(fullgraph=True)`` see an opaque call. Unlike ``mix`` it takes
-the raw ``z_tr`` only: row normalisation happens inside the fused kernel.
+the raw ``z_tr`` only: row normalisation happens inside the fused kernel. z_tr
+and z_tl may be strided views whose last dimension is contiguous (e.g. the two
+halves of the enricher output): their row and batch strides go to the library
+instead of a copy (the reference copies them, ``avey_kernels/ops.py:109-113``).
 
 Nothing here falls back to another implementation: if the shared library is
 missing or refuses the call, the error surfaces to the caller.
@@ -34,6 +37,8 @@ class AveyFwdArgs(ctypes.Structure):
         ('batch', ctypes.c_int64), ('context', ctypes.c_int64), ('features', ctypes.c_int64),
         ('dtype', ctypes.c_int32), ('causal', ctypes.c_int32), ('normalize', ctypes.c_int32),
         ('activation', ctypes.c_int32), ('eps', ctypes.c_double), ('norm_eps', ctypes.c_double),
+        ('z_tr_row_stride', ctypes.c_int64), ('z_tr_batch_stride', ctypes.c_int64),
+        ('z_tl_row_stride', ctypes.c_int64), ('z_tl_batch_stride', ctypes.c_int64),
     ]
 
 
@@ -56,7 +61,7 @@ EXPORTS = {
     'avey_status_string': (ctypes.c_char_p, [ctypes.c_int]),
     'avey_abi_version': (ctypes.c_int, []),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 
@@ -94,17 +99,29 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def row_strides(t):
+    """(row stride, batch stride) in elements of a [B, C, D] operand whose features
+    are contiguous; (0, 0) for a contiguous tensor or None."""
+    if t is None or t.is_contiguous():
+        return 0, 0
+    if t.stride(2) != 1:
+        raise ValueError('z_tr / z_tl need a contiguous last dimension')
+    return t.stride(1), t.stride(0)
+
+
 def make_args(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation):
     batch, context, features = z_tr.shape
     return AveyFwdArgs(
         _ptr(z_tr), _ptr(v), _ptr(z_tl), _ptr(bias), _ptr(valid), _ptr(out),
         batch, context, features, DTYPE_CODES[z_tr.dtype], int(bool(causal)), int(bool(normalize)),
-        ACTIVATION_IDS[activation], float(eps), float(norm_eps))
+        ACTIVATION_IDS[activation], float(eps), float(norm_eps), *row_strides(z_tr), *row_strides(z_tl))
 
 
 def plan(shape, dtype, *, causal, normalize, activation='identity', eps=1e-6, norm_eps=1e-12,
-         has_v=False, has_gate=False, has_bias=False, has_valid=False):
-    """Static tile-table entry for a call, computed on the host (no GPU needed)."""
+         has_v=False, has_gate=False, has_bias=False, has_valid=False, z_tr_strides=(0, 0),
+         z_tl_strides=(0, 0)):
+    """Static tile-table entry for a call, computed on the host (no GPU needed).
+    Strides are (row, batch) in elements; (0, 0) means contiguous."""
     batch, context, features = shape
     # Distinct non-null placeholders: the plan never dereferences pointers.
     base = 1 << 40
@@ -112,7 +129,8 @@ def plan(shape, dtype, *, causal, normalize, activation='identity', eps=1e-6, no
     args = AveyFwdArgs(base, base + step if has_v else None, base + 2 * step if has_gate else None,
                        base + 3 * step if has_bias else None, base + 4 * step if has_valid else None,
                        base + 5 * step, batch, context, features, DTYPE_CODES[dtype], int(causal),
-                       int(normalize), ACTIVATION_IDS[activation], float(eps), float(norm_eps))
+                       int(normalize), ACTIVATION_IDS[activation], float(eps), float(norm_eps),
+                       *z_tr_strides, *z_tl_strides)
     out = AveyFwdPlan()
     st = load().avey_fwd_plan(ctypes.byref(args), ctypes.byref(out))
     if st != 0:
@@ -155,7 +173,8 @@ def launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, ac
 def contextualize(z_tr: torch.Tensor, v: Optional[torch.Tensor], z_tl: Optional[torch.Tensor],
                   bias: Optional[torch.Tensor], valid: Optional[torch.Tensor], eps: float,
                   norm_eps: float, causal: bool, normalize: bool, activation: str) -> torch.Tensor:
-    """out = z_tl * act(mix(z_tr) / den + bias), fused on the GPU; inputs contiguous."""
+    """out = z_tl * act(mix(z_tr) / den + bias), fused on the GPU. z_tr and z_tl may be
+    strided views with a contiguous last dimension; out is contiguous."""
     out = torch.empty_like(z_tr, memory_format=torch.contiguous_format)
     return launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation)
 

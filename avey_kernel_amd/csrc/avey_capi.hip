@@ -24,6 +24,20 @@ size_t elem_size(int dtype) {
   }
 }
 
+// Row and batch strides (elements) of a [B][C][D] operand: row stride 0 means
+// contiguous.
+struct Strides {
+  int64_t row, batch;
+};
+Strides resolve(int64_t row, int64_t batch, const avey_fwd_args& a) {
+  if (row == 0) return {a.features, a.context * a.features};
+  return {row, batch};
+}
+// Elements from the first to one past the last element of a strided operand.
+double span_elems(const Strides& st, const avey_fwd_args& a) {
+  return (double)(a.batch - 1) * (double)st.batch + (double)(a.context - 1) * (double)st.row + (double)a.features;
+}
+
 bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
   if (!a || !b) return false;
   const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
@@ -42,9 +56,17 @@ int validate(const avey_fwd_args* a) {
   if (a->activation < AVEY_ACT_IDENTITY || a->activation > AVEY_ACT_GELU) return AVEY_ERR_ACTIVATION;
   if (!(isfinite(a->eps) && a->eps > 0) || !(isfinite(a->norm_eps) && a->norm_eps > 0)) return AVEY_ERR_EPS;
   if ((a->causal != 0 && a->causal != 1) || (a->normalize != 0 && a->normalize != 1)) return AVEY_ERR_FLAGS;
+  const Strides zs = resolve(a->z_tr_row_stride, a->z_tr_batch_stride, *a);
+  const Strides gs = resolve(a->z_tl_row_stride, a->z_tl_batch_stride, *a);
+  for (const Strides& st : {zs, gs})
+    if (st.row < a->features || st.batch < 0 || st.row > (int64_t(1) << 40) || st.batch > (int64_t(1) << 50))
+      return AVEY_ERR_STRIDE;
+  const double zspan = span_elems(zs, *a), gspan = span_elems(gs, *a);
+  if (zspan * (double)es > 9.0e18 || gspan * (double)es > 9.0e18) return AVEY_ERR_SHAPE;
   const size_t nb = (size_t)n * es;
   const size_t vb = (size_t)a->context * (size_t)a->context * es;
-  if (overlaps(a->out, nb, a->z_tr, nb) || overlaps(a->out, nb, a->z_tl, nb) || overlaps(a->out, nb, a->v, vb) ||
+  if (overlaps(a->out, nb, a->z_tr, (size_t)zspan * es) || overlaps(a->out, nb, a->z_tl, (size_t)gspan * es) ||
+      overlaps(a->out, nb, a->v, vb) ||
       overlaps(a->out, nb, a->bias, (size_t)a->features * es) ||
       overlaps(a->out, nb, a->valid, (size_t)a->batch * (size_t)a->context))
     return AVEY_ERR_ALIAS;
@@ -83,16 +105,21 @@ bool device_ok(int dev) {
 //   * BM halves (down to 16) while the grid would leave CUs of the 256 idle;
 //   * the 16-row variants run 8 waves (warp-specialized), the others 4.
 // The fused kernel addresses memory with 16-byte row chunks and 32-bit buffer
-// offsets, so it also needs D % 8 == 0, 16-byte aligned z_tr / z_tl / out, an
-// 8-byte aligned bias, at most 2^30 elements per batch item and C <= 32768 (V
-// under 2 GiB); other shapes take the generic kernel.
+// offsets, so it also needs D % 8 == 0, 16-byte aligned z_tr / z_tl / out, row
+// and batch strides of z_tr / z_tl that are multiples of 8 elements, an 8-byte
+// aligned bias, batch items spanning under 2^30 elements and C <= 32768 (V under
+// 2 GiB); other shapes take the generic kernel.
 Plan make_plan(const avey_fwd_args& a) {
   Plan pl{};
   const bool low = a.dtype == AVEY_DTYPE_BF16 || a.dtype == AVEY_DTYPE_F16;
   const int nk = slice_steps(a.features);
   const auto al = [](const void* x, uintptr_t n) { return x == nullptr || ((uintptr_t)x & (n - 1)) == 0; };
-  const bool layout = a.features % 8 == 0 && al(a.z_tr, 16) && al(a.z_tl, 16) && al(a.out, 16) && al(a.bias, 8);
-  const bool small_item = a.context * a.features < (int64_t(1) << 30) && a.context <= 32768 &&
+  const Strides zs = resolve(a.z_tr_row_stride, a.z_tr_batch_stride, a);
+  const Strides gs = resolve(a.z_tl_row_stride, a.z_tl_batch_stride, a);
+  const bool strides8 = zs.row % 8 == 0 && zs.batch % 8 == 0 && (a.z_tl == nullptr || (gs.row % 8 == 0 && gs.batch % 8 == 0));
+  const bool layout = a.features % 8 == 0 && al(a.z_tr, 16) && al(a.z_tl, 16) && al(a.out, 16) && al(a.bias, 8) && strides8;
+  const auto item = [&](const Strides& st) { return (a.context - 1) * st.row + a.features; };
+  const bool small_item = item(zs) < (int64_t(1) << 30) && item(gs) < (int64_t(1) << 30) && a.context <= 32768 &&
                           a.batch < (int64_t(1) << 31);
   if (low && nk > 0 && layout && small_item) {
     pl.kernel = 1;
@@ -145,6 +172,7 @@ const char* avey_status_string(int status) {
     case AVEY_ERR_DEVICE: return "current HIP device is not a gfx950 (MI355X) GPU";
     case AVEY_ERR_FLAGS: return "causal and normalize must be 0 or 1";
     case AVEY_ERR_ALIAS: return "out overlaps an input buffer";
+    case AVEY_ERR_STRIDE: return "z_tr / z_tl row stride below features, or a negative stride";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }
@@ -201,6 +229,12 @@ int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, vo
   p.B = a->batch;
   p.C = a->context;
   p.D = a->features;
+  const Strides zs = resolve(a->z_tr_row_stride, a->z_tr_batch_stride, *a);
+  const Strides gs = resolve(a->z_tl_row_stride, a->z_tl_batch_stride, *a);
+  p.zrs = zs.row;
+  p.zbs = zs.batch;
+  p.grs = gs.row;
+  p.gbs = gs.batch;
   p.causal = a->causal;
   p.normalize = a->normalize;
   p.act = a->activation;

@@ -86,11 +86,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)n, kRsrcWord3);
 }
 
-// Resource over rows [row0, rows) of a row-major array with `row_bytes` per row;
-// empty when row0 >= rows.
-__device__ __forceinline__ rsrc_t rows_rsrc(const char* base, int row0, int rows, uint32_t row_bytes) {
+// Resource over rows [row0, rows) of an array whose rows start `stride` bytes apart
+// and hold `row_bytes` bytes; empty when row0 >= rows.
+__device__ __forceinline__ rsrc_t rows_rsrc(const char* base, int row0, int rows, uint32_t stride,
+                                            uint32_t row_bytes) {
   const int n = rows - row0;
-  return make_rsrc(base + (int64_t)row0 * row_bytes, n > 0 ? (uint32_t)n * row_bytes : 0u);
+  return make_rsrc(base + (int64_t)row0 * stride, n > 0 ? (uint32_t)(n - 1) * stride + row_bytes : 0u);
 }
 
 __device__ __forceinline__ u32x4 ld128(rsrc_t r, uint32_t off) {
@@ -288,8 +289,10 @@ __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0x
 
 // FULL: D == 4 * 32 * NK, so every chunk a wave touches lies inside the row.
 // Otherwise chunks at or past D are redirected to kNowhere (D % 8 == 0 makes a
-// chunk wholly in or out).
-template <typename T16, int BM, int NK, bool FULL>
+// chunk wholly in or out). STRIDED: z_tr / z_tl rows and batch items are apart by
+// the strides in FwdParams; otherwise contiguous (a separate instantiation: the
+// runtime strides cost registers, and the 64-row variants then spill more).
+template <typename T16, int BM, int NK, bool FULL, bool STRIDED>
 __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(FwdParams p) {
   typedef Geo<BM, NK> Gm;
   constexpr bool WS = Gm::WS;
@@ -324,10 +327,14 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   const int qt = n_qt - 1 - (int)blockIdx.x / B;
   const int q0 = qt * BM;
   const uint32_t row_bytes = (uint32_t)D * 2u;
-  const char* zb = (const char*)p.z + (int64_t)b * C * row_bytes;
+  // z_tr and z_tl may be strided views (rows and batch items `*stride` apart).
+  const uint32_t zstride = STRIDED ? (uint32_t)p.zrs * 2u : row_bytes;
+  const uint32_t gstride = STRIDED ? (uint32_t)p.grs * 2u : row_bytes;
+  const char* zb = (const char*)p.z + (STRIDED ? (int64_t)b * p.zbs * 2 : (int64_t)b * C * row_bytes);
   const bool has_valid = p.valid != nullptr, has_v = p.v != nullptr;
   const bool has_gate = p.gate != nullptr, has_bias = p.bias != nullptr;
-  const char* gb = has_gate ? (const char*)p.gate + (int64_t)b * C * row_bytes : (const char*)p.z;
+  const char* gb = has_gate ? (const char*)p.gate + (STRIDED ? (int64_t)b * p.gbs * 2 : (int64_t)b * C * row_bytes)
+                             : (const char*)p.z;
   // Absent operands get empty resources (their loads read 0); `or_*` turns those
   // zeros into the neutral value where 0 is not neutral.
   const char* vb = has_valid ? (const char*)p.valid + (int64_t)b * C : (const char*)p.z;
@@ -353,12 +360,13 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   auto qrows_base = [&](int j) -> char* { return j == 0 ? ((R == 3 ? slot2 : slot1) + w * SLICE) : (ovf + w * SLICE); };
   auto erows_base = [&](int j) -> char* { return (j == 0 ? slot0 : slot1) + w * SLICE; };
 
-  // Global byte offset (from a region's first row) of slice position pos, i.e. row
-  // pos / CPRP, chunk swizzle(row, pos % CPRP); kNowhere past the slice or past D.
-  auto goff = [&](int pos) -> uint32_t {
+  // Global byte offset (from a region's first row; rows `stride` bytes apart) of
+  // slice position pos, i.e. row pos / CPRP, chunk swizzle(row, pos % CPRP);
+  // kNowhere past the slice or past D.
+  auto goff = [&](int pos, uint32_t stride) -> uint32_t {
     const int r = pos / CPRP, c = swzc<G>(r, pos % CPRP);
     const int col = fw + 8 * c;
-    return (c < CPR && (FULL || col < D)) ? (uint32_t)r * row_bytes + (uint32_t)col * 2u : kNowhere;
+    return (c < CPR && (FULL || col < D)) ? (uint32_t)r * stride + (uint32_t)col * 2u : kNowhere;
   };
   constexpr int P = Gm::P, RPP = Gm::RPP;
   // The DMA lane offsets stay in registers unless the variant's registers are
@@ -367,7 +375,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   uint32_t kof_live[P];
   if constexpr (KOF_LIVE) {
 #pragma unroll
-    for (int j = 0; j < P; ++j) kof_live[j] = goff(64 * j + lane);
+    for (int j = 0; j < P; ++j) kof_live[j] = goff(64 * j + lane, zstride);
   }
   // LDS byte offsets of this lane's fragments inside a slice (see Geo):
   //   a1: similarity operands, row li, chunk 4 s + lg          (s % (G / 4) picks the entry)
@@ -419,7 +427,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
       // Recomputed from an opaque lane index, so the compiler cannot keep them live.
       const int ln = (int)opaque((uint32_t)lane);
 #pragma unroll
-      for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + ln);
+      for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + ln, zstride);
     }
   };
   // DMA instruction j (of KDMA) of key tile t into this wave's part of a ring slot.
@@ -428,13 +436,13 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // free slot have been seen to make the compiler drop the wait that a later read
   // of the other slot needs (it read a tile whose copies were still in flight).
   auto fetch_key_part = [&](int t, char* dst, int j, const uint32_t (&kof)[P]) {
-    dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, row_bytes), dst + 1024 * j, kof[j % P]);
+    dma16(rows_rsrc(zb, t * kBN + RPP * (j / P), C, zstride, row_bytes), dst + 1024 * j, kof[j % P]);
   };
   auto fetch_valid = [&](int t, auto slot, bool live = true) {
     constexpr int I = decltype(slot)::value;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
-      zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, live ? valid_rows : 0, 1u), (uint32_t)li);
+      zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, live ? valid_rows : 0, 1u, 1u), (uint32_t)li);
   };
   auto fetch_keys = [&](int t, auto slot) {
     uint32_t kof[P];
@@ -443,15 +451,16 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     for (int j = 0; j < KDMA; ++j) fetch_key_part(t, slot_base(slot), j, kof);
     fetch_valid(t, slot);
   };
-  // BM rows of a [B][C][D] tensor from row q0 into a row region (prologue: the
-  // queries; tail: the gate).
-  auto fetch_rows = [&](const char* src, auto region) {
+  // BM rows (`stride` bytes apart) of a batch item from row q0 into a row region
+  // (prologue: the queries; tail: the gate).
+  auto fetch_rows = [&](const char* src, uint32_t stride, auto region) {
     uint32_t kof[P];
 #pragma unroll
-    for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
+    for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane, stride);
 #pragma unroll
     for (int j = 0; j < BM * CPRP / 64; ++j)
-      dma16(rows_rsrc(src, q0 + RPP * (j / P), C, row_bytes), region(j / KDMA) + 1024 * (j % KDMA), kof[j % P]);
+      dma16(rows_rsrc(src, q0 + RPP * (j / P), C, stride, row_bytes), region(j / KDMA) + 1024 * (j % KDMA),
+            kof[j % P]);
   };
   // V entries of tile k0 for this wave's units (raw 16-bit words, two per dword): the
   // lane's four keys are adjacent, so with an even context one dword-aligned 8-byte
@@ -473,7 +482,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
   if (do_mma) {
-    fetch_rows((const char*)zb, qrows_base);
+    fetch_rows((const char*)zb, zstride, qrows_base);
     fetch_keys(0, IC<0>{});
     if constexpr (R == 3) {
       if (1 < nkt) fetch_keys(1, IC<1>{});
@@ -488,17 +497,21 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   const bool gate_fits = (uint64_t)B * (uint64_t)C * row_bytes <= (8ull << 20);
   const int touch_t = gate_fits ? 0 : nkt - kTouchLead;  // the iteration that touches; < 1: here
   auto touch_gate = [&]() {  // by the 256 lanes of the product waves
-    const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), row_bytes);
-    constexpr int kTouches = (BM * 4 * 32 * NK * 2 / 128 + kThreads - 1) / kThreads;  // lines over 256 lanes
+    const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), gstride, row_bytes);
+    constexpr int kLines = 4 * 32 * NK * 2 / 128;                          // 128-byte lines per row
+    constexpr int kTouches = (BM * kLines + kThreads - 1) / kThreads;     // lines over 256 lanes
 #pragma unroll
-    for (int i = 0; i < kTouches; ++i) dma4(r, touch_sink, (uint32_t)(i * kThreads + tid) * 128u);
+    for (int i = 0; i < kTouches; ++i) {
+      const uint32_t line = (uint32_t)(i * kThreads + tid), c = line % kLines;
+      dma4(r, touch_sink, c * 128u < row_bytes ? (line / kLines) * gstride + c * 128u : kNowhere);
+    }
   };
-  if (has_gate && touch_t < 1) touch_gate();
+  if (do_mma && has_gate && touch_t < 1) touch_gate();
   u32x4 qf[QB][NK];
   if (do_mma) {
   uint32_t qv[QB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
+  for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u, 1u), (uint32_t)li);
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const bool ok = (16 * qb + li < C - q0) && ((qv[qb] | or_valid) != 0u);
@@ -829,7 +842,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
     wait_lds_reads();
   }
-  if (has_gate) fetch_rows(gb, erows_base);
+  if (has_gate) fetch_rows(gb, gstride, erows_base);
   // The epilogue's bias words and validity bytes, now that the query fragments are
   // dead: their latency hides behind the last reduction and mixing product.
   u32x2 bw[NT];
@@ -842,7 +855,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
       bw[t2] = ld64(rbias, (FULL || f < D) ? (uint32_t)f * 2u : kNowhere);
     }
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u), (uint32_t)li);
+    for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u, 1u), (uint32_t)li);
   }
   if constexpr (RED) stage_b(nkt - 1);
   lds_barrier();
@@ -930,39 +943,39 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   const char* ob = (const char*)p.out + (int64_t)b * C * row_bytes;
   uint32_t kof[P];
 #pragma unroll
-  for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane);
+  for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane, row_bytes);
 #pragma unroll
   for (int j = 0; j < BM * CPRP / 64; ++j) {
     const u32x4 v = *reinterpret_cast<const u32x4*>(erows_base(j / KDMA) + 1024 * (j % KDMA) + 16 * lane);
-    st128(v, rows_rsrc(ob, q0 + RPP * (j / P), C, row_bytes), kof[j % P]);
+    st128(v, rows_rsrc(ob, q0 + RPP * (j / P), C, row_bytes, row_bytes), kof[j % P]);
   }
 }
 
-// Instantiates and launches fused_fwd_kernel<T16, BM, NK, FULL> for one BM and
-// type; defined in avey_fused_bm{16,32,64}_{bf16,f16}.hip so the variants compile
-// in parallel.
-template <typename T16, int BM>
+// Instantiates and launches fused_fwd_kernel<T16, BM, NK, FULL, STRIDED> for one
+// BM, type and stride kind; defined in avey_fused_bm{16,32,64}_{bf16,f16}[_strided].hip
+// so the variants compile in parallel.
+template <typename T16, int BM, bool STRIDED>
 hipError_t launch_fused_bm(const FwdParams& p, int nk, int64_t grid, hipStream_t s);
 
-template <typename T16, int BM, int NK>
+template <typename T16, int BM, int NK, bool STRIDED>
 hipError_t launch_fused_one(const FwdParams& p, int64_t grid, hipStream_t s) {
   if (p.D == 4 * 32 * NK)
-    fused_fwd_kernel<T16, BM, NK, true><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
+    fused_fwd_kernel<T16, BM, NK, true, STRIDED><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
   else
-    fused_fwd_kernel<T16, BM, NK, false><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
+    fused_fwd_kernel<T16, BM, NK, false, STRIDED><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
   return hipGetLastError();
 }
 
-template <typename T16, int BM>
+template <typename T16, int BM, bool STRIDED>
 hipError_t launch_fused_nk(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
   switch (nk) {
-    case 1: return launch_fused_one<T16, BM, 1>(p, grid, s);
-    case 2: return launch_fused_one<T16, BM, 2>(p, grid, s);
-    case 3: return launch_fused_one<T16, BM, 3>(p, grid, s);
-    case 4: return launch_fused_one<T16, BM, 4>(p, grid, s);
-    case 6: return launch_fused_one<T16, BM, 6>(p, grid, s);
+    case 1: return launch_fused_one<T16, BM, 1, STRIDED>(p, grid, s);
+    case 2: return launch_fused_one<T16, BM, 2, STRIDED>(p, grid, s);
+    case 3: return launch_fused_one<T16, BM, 3, STRIDED>(p, grid, s);
+    case 4: return launch_fused_one<T16, BM, 4, STRIDED>(p, grid, s);
+    case 6: return launch_fused_one<T16, BM, 6, STRIDED>(p, grid, s);
     case 8:
-      if constexpr (BM <= 32) return launch_fused_one<T16, BM, 8>(p, grid, s);
+      if constexpr (BM <= 32) return launch_fused_one<T16, BM, 8, STRIDED>(p, grid, s);
       return hipErrorInvalidConfiguration;
     default: return hipErrorInvalidConfiguration;
   }

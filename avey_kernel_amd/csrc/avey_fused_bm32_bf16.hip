@@ -1,11 +1,11 @@
-// Fused kernel variants with 32 query rows per workgroup, bf16.
+// Fused kernel variants with 32 query rows per workgroup, bf16, contiguous operands.
 #include "avey_fused.h"
 
 namespace avey {
 
 template <>
-hipError_t launch_fused_bm<__bf16, 32>(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
-  return launch_fused_nk<__bf16, 32>(p, nk, grid, s);
+hipError_t launch_fused_bm<__bf16, 32, false>(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
+  return launch_fused_nk<__bf16, 32, false>(p, nk, grid, s);
 }
 
 }  // namespace avey

@@ -1,0 +1,11 @@
+// Fused kernel variants with 64 query rows per workgroup, bf16, strided z_tr / z_tl.
+#include "avey_fused.h"
+
+namespace avey {
+
+template <>
+hipError_t launch_fused_bm<__bf16, 64, true>(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
+  return launch_fused_nk<__bf16, 64, true>(p, nk, grid, s);
+}
+
+}  // namespace avey

@@ -1,11 +1,11 @@
-// Fused kernel variants with 64 query rows per workgroup, f16.
+// Fused kernel variants with 64 query rows per workgroup, f16, contiguous operands.
 #include "avey_fused.h"
 
 namespace avey {
 
 template <>
-hipError_t launch_fused_bm<_Float16, 64>(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
-  return launch_fused_nk<_Float16, 64>(p, nk, grid, s);
+hipError_t launch_fused_bm<_Float16, 64, false>(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
+  return launch_fused_nk<_Float16, 64, false>(p, nk, grid, s);
 }
 
 }  // namespace avey

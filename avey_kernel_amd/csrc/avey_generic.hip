@@ -12,18 +12,19 @@
 namespace avey {
 
 // inv[b*C + j] = 1 / max(||z_j||_2, norm_eps); padded rows count as zero rows
-// (ops.py:64-68). One wave per row.
+// (ops.py:64-68). One wave per row; rows `zrs` and batch items `zbs` elements apart.
 template <typename T>
 __global__ __launch_bounds__(256) void row_inv_norm_kernel(const T* __restrict__ z, const uint8_t* __restrict__ valid,
                                                            typename Elem<T>::acc* __restrict__ inv, int64_t rows,
-                                                           int64_t D, double norm_eps) {
+                                                           int64_t C, int64_t D, int64_t zrs, int64_t zbs,
+                                                           double norm_eps) {
   typedef typename Elem<T>::acc A;
   const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   if (row >= rows) return;
   A ss = 0;
   if (!valid || valid[row]) {
-    const T* zr = z + row * D;
+    const T* zr = z + (row / C) * zbs + (row % C) * zrs;
     for (int64_t f = lane; f < D; f += 64) {
       A x = Elem<T>::to_acc(zr[f]);
       ss += x * x;
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
   const int64_t qt = ((int64_t)blockIdx.x / nft) % nqt;
   const int64_t b = (int64_t)blockIdx.x / nft / nqt;
   const int64_t q0 = qt * BQ, f0 = ft * BF;
-  const T* zb = (const T*)p.z + b * C * D;
+  const T* zb = (const T*)p.z + b * p.zbs;  // row r at zb + r * p.zrs
   const uint8_t* vb = p.valid ? p.valid + b * C : nullptr;
   const A* inv = (const A*)p.work + b * C;
   const T* vw = (const T*)p.v;
@@ -83,8 +84,8 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
         const int r = e / DC, c = e % DC;
         const int64_t f = d0 + c;
         const int64_t q = q0 + r, k = k0 + r;
-        qs[r][c] = (f < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * D + f]) : A(0);
-        ks[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * D + f]) : A(0);
+        qs[r][c] = (f < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * p.zrs + f]) : A(0);
+        ks[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + f]) : A(0);
       }
       __syncthreads();
 #pragma unroll 8
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     for (int e = t; e < BK * BF; e += 256) {
       const int r = e / BF, c = e % BF;
       const int64_t k = k0 + r, f = f0 + c;
-      kf[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * D + f]) : A(0);
+      kf[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + f]) : A(0);
     }
     __syncthreads();
     if (p.normalize && t < BQ) {
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     if (p.normalize) y = y / dd;
     if (bias) y += Elem<T>::to_acc(bias[f]);
     y = activate<A>(y, p.act);
-    if (gate) y *= qv ? Elem<T>::to_acc(gate[(b * C + q) * D + f]) : A(0);
+    if (gate) y *= qv ? Elem<T>::to_acc(gate[b * p.gbs + q * p.grs + f]) : A(0);
     out[f] = Elem<T>::from_acc(qv ? y : A(0));
   }
 }
@@ -143,7 +144,7 @@ template <typename T>
 static hipError_t launch_generic_t(const FwdParams& p, hipStream_t s) {
   const int64_t rows = p.B * p.C;
   row_inv_norm_kernel<T><<<dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s>>>(
-      (const T*)p.z, p.valid, (typename Elem<T>::acc*)p.work, rows, p.D, p.norm_eps);
+      (const T*)p.z, p.valid, (typename Elem<T>::acc*)p.work, rows, p.C, p.D, p.zrs, p.zbs, p.norm_eps);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t grid = cdiv(p.C, 16) * cdiv(p.D, 64) * p.B;

@@ -18,6 +18,8 @@ struct FwdParams {
   void* out;            // [B][C][D]
   void* work;           // scratch (generic path: per-row inverse norms)
   int64_t B, C, D;
+  int64_t zrs, zbs;     // z_tr row / batch strides (elements)
+  int64_t grs, gbs;     // z_tl row / batch strides (elements)
   int32_t causal, normalize, act;
   double eps, norm_eps;
 };

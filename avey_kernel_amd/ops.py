@@ -127,6 +127,11 @@ def _fused_device(t):
     return getattr(props, 'gcnArchName', '').startswith('gfx950')
 
 
+def _rows(t):
+    """t itself when its features are contiguous (any row / batch strides), else a copy."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
 def _dispatch(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation, backend,
               output_tile, autotune):
     _validate(z_tr, v, z_tl, bias, valid, eps, norm_eps, activation, backend, output_tile, autotune)
@@ -138,10 +143,13 @@ def _dispatch(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, acti
                          'inference inputs; use backend="torch" for autograd or other devices')
     if backend == 'torch' or not fused_ok:
         return _eager(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation)
-    # The fused path: contiguous operands (ops.py:109-113 does the same), one launch.
+    # The fused path, one launch. z_tr / z_tl go in as they are when their features
+    # are contiguous (strided views such as the halves of the enricher output: the
+    # library takes their row and batch strides), where ops.py:109-113 copies them;
+    # the other operands are made contiguous as there.
     return torch.ops.avey_kernels.contextualize(
-        z_tr.contiguous(), v.contiguous() if v is not None else None,
-        z_tl.contiguous() if z_tl is not None else None,
+        _rows(z_tr), v.contiguous() if v is not None else None,
+        _rows(z_tl) if z_tl is not None else None,
         bias.contiguous() if bias is not None else None,
         valid.contiguous() if valid is not None else None,
         float(eps), float(norm_eps), bool(causal), bool(normalize), activation)

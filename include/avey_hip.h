@@ -22,7 +22,10 @@
  * Conventions
  *   - All tensor pointers are device pointers owned by the caller. The
  *     library never allocates, frees or keeps pointers after a call returns.
- *   - z_tr, z_tl, out: [batch][context][features], row-major, contiguous.
+ *   - z_tr, z_tl, out: [batch][context][features], features contiguous.
+ *     z_tr and z_tl may be strided views (row and batch strides in the
+ *     arguments; e.g. the two halves of the enricher output, which the
+ *     reference copies with .contiguous(), ops.py:109-113); out is contiguous.
  *     v: [context][context] indexed [query][key], shared by the batch.
  *     bias: [features]. valid: [batch][context] bytes (0 = padded row).
  *     z_tr, z_tl, v, bias and out share one element type (ops.py:39-43).
@@ -40,7 +43,7 @@
 extern "C" {
 #endif
 
-#define AVEY_ABI_VERSION 1
+#define AVEY_ABI_VERSION 2
 
 /* Element type of z_tr / z_tl / v / bias / out. */
 enum avey_dtype {
@@ -70,6 +73,7 @@ enum avey_status {
   AVEY_ERR_DEVICE = -7,           /* current device is not gfx950 */
   AVEY_ERR_FLAGS = -8,            /* causal / normalize not 0 or 1 */
   AVEY_ERR_ALIAS = -9,            /* out overlaps an input */
+  AVEY_ERR_STRIDE = -10,          /* a row stride below features, or a negative stride */
 };
 
 typedef struct avey_fwd_args {
@@ -88,6 +92,16 @@ typedef struct avey_fwd_args {
   int32_t activation;   /* enum avey_activation */
   double eps;           /* denominator epsilon (used when normalize = 1) */
   double norm_eps;      /* F.normalize clamp of the row norm */
+  /* Strides of z_tr and z_tl in elements (ABI 2). A row stride of 0 means
+   * contiguous (row stride = features, batch stride = context * features) and
+   * the batch stride is then ignored; otherwise the row stride must be at least
+   * `features` and the batch stride is used as given (>= 0). The fused MFMA
+   * kernel needs both strides to be multiples of 8 (16-byte rows); other
+   * strides take the generic kernel. */
+  int64_t z_tr_row_stride;
+  int64_t z_tr_batch_stride;
+  int64_t z_tl_row_stride;
+  int64_t z_tl_batch_stride;
 } avey_fwd_args;
 
 /* Kernel choice and launch geometry for one call; filled by avey_fwd_plan. */

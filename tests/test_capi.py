@@ -38,13 +38,13 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_hip.EXPORTS), declared ^ set(_hip.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.avey_abi_version() == 1
+    assert lib.avey_abi_version() == _hip.ABI_VERSION == 2
 
 
 def _args(**over):
     base = dict(z_tr=1 << 40, v=None, z_tl=None, bias=None, valid=None, out=(1 << 40) + (1 << 36),
                 batch=2, context=35, features=37, dtype=2, causal=1, normalize=0, activation=0, eps=1e-6,
-                norm_eps=1e-12)
+                norm_eps=1e-12, z_tr_row_stride=0, z_tr_batch_stride=0, z_tl_row_stride=0, z_tl_batch_stride=0)
     base.update(over)
     return _hip.AveyFwdArgs(*[base[f] for f, _ in _hip.AveyFwdArgs._fields_])
 
@@ -56,6 +56,12 @@ def _args(**over):
     (dict(eps=0.0), -5), (dict(norm_eps=float('nan')), -5), (dict(eps=float('inf')), -5),
     (dict(causal=2), -8), (dict(normalize=-1), -8),
     (dict(out=(1 << 40) + 64), -9),
+    # Strided z_tr / z_tl: a row stride below `features` or a negative batch stride.
+    (dict(z_tr_row_stride=36), -10), (dict(z_tr_row_stride=74, z_tr_batch_stride=-1), -10),
+    (dict(z_tl=(1 << 41), z_tl_row_stride=1), -10),
+    # out inside z_tr's strided span (rows 74 elements apart: 2 * 35 * 74 * 2 bytes)
+    # though past what a contiguous z_tr would cover (2 * 35 * 37 * 2 bytes).
+    (dict(z_tr_row_stride=74, z_tr_batch_stride=35 * 74, out=(1 << 40) + 2 * 35 * 37 * 2 + 64), -9),
 ])
 def test_argument_errors_return_status_before_any_device_work(over, code):
     lib = _lib()
@@ -104,3 +110,30 @@ def test_static_tile_table():
         g = _hip.plan((2, 64, 64), dt, causal=True, normalize=False)
         assert g['kernel'] == 'generic_valu' and g['workspace_bytes'] == 2 * 64 * (8 if dt == torch.float64 else 4)
     assert _hip.plan((1, 8, 4096), torch.bfloat16, causal=False, normalize=True)['kernel'] == 'generic_valu'
+
+
+def test_strided_views_choose_the_kernel_by_stride_alignment():
+    _lib()
+    shape = (16, 256, 768)
+    # The two halves of a [B, C, 2D] enricher output: rows 2D apart, items C * 2D apart.
+    halves = (2 * 768, 256 * 2 * 768)
+    p = _hip.plan(shape, torch.bfloat16, causal=True, normalize=False, has_gate=True, z_tr_strides=halves,
+                  z_tl_strides=halves)
+    q = _hip.plan(shape, torch.bfloat16, causal=True, normalize=False, has_gate=True)
+    assert p == q and p['kernel'] == 'fused_mfma'
+    # Strides that are not whole 16-byte chunks take the generic kernel (any stride).
+    for zs, gs in (((772, 256 * 772), (0, 0)), ((0, 0), (776, 256 * 776 + 4))):
+        r = _hip.plan(shape, torch.bfloat16, causal=True, normalize=False, has_gate=True, z_tr_strides=zs,
+                      z_tl_strides=gs)
+        assert r['kernel'] == 'generic_valu', (zs, gs)
+    # A batch item spanning 2^30 elements or more also leaves the fused kernel.
+    wide = _hip.plan((1, 32768, 512), torch.bfloat16, causal=False, normalize=True, z_tr_strides=(32776, 0))
+    assert wide['kernel'] == 'generic_valu'
+
+
+def test_row_strides_of_torch_views():
+    x = torch.empty(2, 5, 16)
+    assert _hip.row_strides(x) == (0, 0) and _hip.row_strides(None) == (0, 0)
+    assert _hip.row_strides(x[..., 8:]) == (16, 80)
+    with pytest.raises(ValueError):
+        _hip.row_strides(x.transpose(1, 2))

@@ -79,7 +79,7 @@ def _assert_close(out, want, dtype, label='', cond=None):
 
 def test_library_is_loaded_and_device_supported():
     lib = _hip.load()
-    assert lib.avey_abi_version() == 1
+    assert lib.avey_abi_version() == _hip.ABI_VERSION
     assert _hip.device_supported(DEV)
 
 
@@ -241,6 +241,65 @@ def test_noncontiguous_inputs_match_contiguous():
     out = avey_b(z, backend='hip')
     ref = avey_b(z.contiguous(), backend='hip')
     assert torch.equal(out, ref)
+
+
+# Strided z_tr / z_tl views are read in place (rows and batch items at their own
+# strides) and must give the contiguous call's result bit for bit. Cases: the two
+# halves of a [B, C, 2D] enricher output on each fused variant (BM 16 / 32 / 64 by
+# the plan's grid rule), a view at an offset, strides that are not whole 16-byte
+# chunks (generic kernel), fp32 (generic kernel), and padding with NaN rows.
+@pytest.mark.parametrize('batch,context,d,dtype,extra,label', [
+    (2, 70, 200, torch.bfloat16, 0, 'BM16 halves'),
+    (32, 256, 768, torch.bfloat16, 0, 'BM32 halves'),
+    (64, 256, 512, torch.float16, 0, 'BM64 halves'),
+    (3, 45, 64, torch.bfloat16, 8, 'offset view'),
+    (3, 45, 64, torch.bfloat16, 4, 'odd stride -> generic'),
+    (2, 33, 48, torch.float32, 0, 'fp32 generic'),
+])
+def test_strided_views_read_in_place(batch, context, d, dtype, extra, label):
+    g = torch.Generator().manual_seed(context * 7 + d)
+    width = 2 * d + extra
+    x = torch.randn(batch, context, width, generator=g).to(DEV, dtype)
+    z_tl, z_tr = x[..., extra:extra + d], x[..., extra + d:extra + 2 * d]
+    assert not z_tr.is_contiguous() and z_tr.stride() == (context * width, width, 1)
+    v = ((torch.rand(context, context, generator=g) * 2 - 1) / context ** 0.5).to(DEV, dtype)
+    bias = (torch.randn(d, generator=g) * 0.1).to(DEV, dtype)
+    lengths = torch.randint(context // 2, context + 1, (batch,), generator=g)
+    valid = (torch.arange(context)[None, :] < lengths[:, None]).to(DEV)
+    kind = _hip.plan((batch, context, d), dtype, causal=True, normalize=False, z_tr_strides=z_tr.stride()[1::-1],
+                     z_tl_strides=z_tl.stride()[1::-1])['kernel']
+    assert (kind == 'fused_mfma') == (dtype != torch.float32 and extra % 8 == 0), (label, kind)
+    # Same kernel as for contiguous copies: bitwise equal; otherwise (strides that
+    # are not whole 16-byte chunks send bf16 to the generic kernel) the oracle.
+    same_kernel = kind == _hip.plan((batch, context, d), dtype, causal=True, normalize=False)['kernel']
+    cases = [dict(v=v, causal=True, normalize=False, valid=None, eps=1e-6, act='silu'),
+             dict(v=None, causal=False, normalize=True, valid=valid, eps=0.25, act='gelu')]
+    for c in cases:
+        if c['valid'] is not None:
+            x[~c['valid']] = float('nan')  # NaN in the padded rows of both halves
+        rest = (bias, c['valid'], c['eps'], 1e-12, c['causal'], c['normalize'], c['act'])
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated()
+        out = torch.ops.avey_kernels.contextualize(z_tr, c['v'], z_tl, *rest)
+        torch.cuda.synchronize()
+        # Nothing outlives the call but the output: the views were not copied.
+        assert torch.cuda.memory_allocated() - before <= out.numel() * out.element_size() + 4096, label
+        if same_kernel:
+            want = torch.ops.avey_kernels.contextualize(z_tr.contiguous(), c['v'], z_tl.contiguous(), *rest)
+            assert torch.equal(out, want), (label, c['normalize'])
+        else:
+            zc = z_tr.nan_to_num()  # the oracle zeroes padded rows itself
+            want = _oracle(zc, c['v'], z_tl.nan_to_num(), bias, c['valid'], eps=c['eps'], causal=c['causal'],
+                           normalize=c['normalize'], act=c['act'])
+            cond = orc.row_condition(_np(zc), c['valid'].cpu().numpy(), eps=c['eps']) if c['normalize'] else None
+            _assert_close(out, want, dtype, label, cond)
+        # The public API hands the views to the library unchanged.
+        if c['normalize']:
+            api = avey_b(z_tr, z_tl=z_tl, bias=bias, valid=c['valid'], eps=c['eps'], activation=c['act'],
+                         backend='hip')
+        else:
+            api = avey(z_tr, c['v'], z_tl=z_tl, bias=bias, activation=c['act'], backend='hip')
+        assert torch.equal(api, out), (label, 'api')
 
 
 def test_gradient_request_falls_back_and_hip_backend_refuses():
