@@ -481,11 +481,20 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
+  // In the 8-wave variants the helpers copy tile 1 (first thing in their program),
+  // so that the product waves reach the query norms and A(0) after issuing only the
+  // query rows and tile 0 (the copy queue is in issue order); the product waves still
+  // load tile 1's validity bytes, which they use.
   if (do_mma) {
     fetch_rows((const char*)zb, zstride, qrows_base);
     fetch_keys(0, IC<0>{});
     if constexpr (R == 3) {
-      if (1 < nkt) fetch_keys(1, IC<1>{});
+      if (1 < nkt) {
+        if constexpr (WS)
+          fetch_valid(1, IC<1>{});
+        else
+          fetch_keys(1, IC<1>{});
+      }
     }
   }
   // The gate rows are first read in the tail; one touch per 128-byte line ahead of
@@ -737,6 +746,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     if (helper) {
       // The helpers' program: the same barriers as the product waves', in order.
       constexpr int KH = KDMA / 2;
+      if (R == 3 && 1 < nkt) refill_part(1, IC<1>{}, IC<0>{}, IC<KDMA>{});  // tile 1 (see the prologue)
       load_v(0, vv);
       lds_barrier();  // A(0) done, the query rows in slot R-1 consumed
       if (R - 1 < nkt) refill_part(R - 1, IC<R - 1>{}, IC<0>{}, IC<KDMA>{});
