@@ -175,6 +175,12 @@ def contextualize(z_tr: torch.Tensor, v: Optional[torch.Tensor], z_tl: Optional[
                   norm_eps: float, causal: bool, normalize: bool, activation: str) -> torch.Tensor:
     """out = z_tl * act(mix(z_tr) / den + bias), fused on the GPU. z_tr and z_tl may be
     strided views with a contiguous last dimension; out is contiguous."""
+    # Callers such as Inductor hand over whatever layouts their graph chose: views
+    # with contiguous features go through as they are, anything else is made so.
+    z_tr = z_tr if z_tr.stride(-1) == 1 else z_tr.contiguous()
+    if z_tl is not None and z_tl.stride(-1) != 1:
+        z_tl = z_tl.contiguous()
+    v, bias, valid = (None if t is None else t.contiguous() for t in (v, bias, valid))
     out = torch.empty_like(z_tr, memory_format=torch.contiguous_format)
     return launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation)
 

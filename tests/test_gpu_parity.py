@@ -14,6 +14,8 @@ size, size-independent properties (bitwise determinism, causal rows blind to
 the future) and HIP-graph replay.
 """
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -300,6 +302,55 @@ def test_strided_views_read_in_place(batch, context, d, dtype, extra, label):
         else:
             api = avey(z_tr, c['v'], z_tl=z_tl, bias=bias, activation=c['act'], backend='hip')
         assert torch.equal(api, out), (label, 'api')
+
+
+def test_inductor_compiles_the_op_as_an_extern_call():
+    # torch.compile(fullgraph=True) with the default (Inductor) backend: the enricher
+    # split, the fused op and a following pointwise op in one graph; the op runs as
+    # an opaque extern call and the result matches eager bitwise.
+    g = torch.Generator().manual_seed(11)
+    d = 200
+    x = torch.randn(2, 70, 2 * d, generator=g).to(DEV, torch.bfloat16)
+    v = ((torch.rand(70, 70, generator=g) * 2 - 1) / 70 ** 0.5).to(DEV, torch.bfloat16)
+    b = (torch.randn(d, generator=g) * 0.1).to(DEV, torch.bfloat16)
+
+    def fn(x, v, b):
+        z_tl, z_tr = x[..., :d], x[..., d:]
+        return avey(z_tr, v, z_tl=z_tl, bias=b, activation='silu', backend='hip') * 2.0
+
+    eager = fn(x, v, b)
+    compiled = torch.compile(fn, fullgraph=True)
+    for _ in range(2):
+        assert torch.equal(compiled(x, v, b), eager)
+
+
+def test_first_call_of_a_process_can_be_graph_captured():
+    # The very first call in a fresh process happens under HIP-graph capture: the
+    # library loads, checks the device and launches without any host
+    # synchronisation or stream-ordered allocation of its own.
+    import subprocess
+    import sys
+    code = """
+import torch
+from avey_kernel_amd import avey
+g = torch.Generator().manual_seed(5)
+z = torch.randn(2, 96, 256, generator=g).to('cuda', torch.bfloat16)
+v = (torch.rand(96, 96, generator=g) / 10).to('cuda', torch.bfloat16)
+graph = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(graph):
+        out = avey(z, v, backend='hip')
+for _ in range(3):
+    graph.replay()
+torch.cuda.synchronize()
+ref = avey(z, v, backend='hip')
+print('EQUAL' if torch.equal(out, ref) else 'DIFFER', flush=True)
+"""
+    res = subprocess.run([sys.executable, '-c', code], capture_output=True, text=True, timeout=100,
+                         cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    assert res.returncode == 0, res.stderr[-2000:]
+    assert res.stdout.strip().endswith('EQUAL'), res.stdout[-500:]
 
 
 def test_gradient_request_falls_back_and_hip_backend_refuses():
