@@ -128,8 +128,7 @@ Plan make_plan(const avey_fwd_args& a) {
     int bm = nk <= 6 ? 64 : 32;
     while (bm > 16 && cdiv(a.context, bm) * a.batch < 256) bm /= 2;
     pl.bm = bm;
-    // The 16-row variants are warp-specialized: 4 product waves and 4 helper waves.
-    pl.threads = bm == 16 ? 512 : 256;
+    pl.threads = fused_threads(bm, nk);
     const int64_t nqt = cdiv(a.context, bm);
     pl.grid = nqt * a.batch;
     pl.work_bytes = 0;

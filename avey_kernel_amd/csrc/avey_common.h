@@ -83,6 +83,18 @@ __device__ __forceinline__ float activate<float>(float x, int act) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Waves of the fused kernel's (BM query rows, NK 32-feature steps per slice)
+// variants. The 16-row ones split roles over 8 waves (4 product waves, 4 helpers);
+// 32- and 64-row ones split their query blocks over 8 waves where a wave's half of
+// the state fits 256 registers (up to 192 features per slice with 32 rows, 128
+// with 64), and otherwise run 4 waves of 512 registers.
+__host__ __device__ constexpr bool fused_query_split(int bm, int nk) {
+  return (bm == 32 && nk <= 6) || (bm == 64 && nk <= 4);
+}
+__host__ __device__ constexpr int fused_threads(int bm, int nk) {
+  return (bm == 16 || fused_query_split(bm, nk)) ? 512 : 256;
+}
+
 // Key tiles a query tile visits. Causal skipping keeps the tile holding the
 // diagonal and drops every tile that starts after the block's last query
 // (the reference rule, avey_kernels/_triton.py:38-50).

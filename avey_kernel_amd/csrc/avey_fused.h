@@ -242,7 +242,16 @@ struct Geo {
   // key reciprocals and the refill DMAs, so that none of these stalls the MFMAs, and
   // each SIMD holds two waves whose stalls the other fills.
   static constexpr bool WS = BM == 16;
-  static constexpr int THREADS = (WS ? 2 : 1) * kThreads;
+  // Query split (the 32- and 64-row variants whose halved state fits 256 registers):
+  // 8 waves, waves w and w + 4 both serve feature slice w, each for half of the query
+  // blocks. Every wave runs every stage on its half (the key rows of a slice are read
+  // by both), so a wave holds half the accumulators and each SIMD holds two waves
+  // whose stalls the other fills. The others keep 4 waves of 512 registers.
+  static constexpr bool QS = fused_query_split(BM, NK);
+  static constexpr int THREADS = fused_threads(BM, NK);
+  static_assert(THREADS == (WS || QS ? 2 : 1) * kThreads, "wave count");
+  static constexpr int QBW = QS ? QB / 2 : QB;        // query blocks per wave
+  static constexpr int KD = QS ? KDMA / 2 : KDMA;     // refill copies per wave per tile
 };
 
 template <int G>
@@ -295,10 +304,13 @@ __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0x
 template <typename T16, int BM, int NK, bool FULL, bool STRIDED>
 __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(FwdParams p) {
   typedef Geo<BM, NK> Gm;
-  constexpr bool WS = Gm::WS;
+  constexpr bool WS = Gm::WS, QS = Gm::QS;
   constexpr int QB = Gm::QB, DS = Gm::DS, NT = Gm::NT, CPR = Gm::CPR, CPRP = Gm::CPRP, G = Gm::G;
   constexpr int SLICE = Gm::SLICE, TILE = Gm::TILE, R = Gm::R, KDMA = Gm::KDMA;
-  constexpr int UNITS = 2 * QB, UPW = (UNITS + kWaves - 1) / kWaves;
+  constexpr int QBW = Gm::QBW, KD = Gm::KD;
+  // Reduction units (query block, key half) are shared by RW waves.
+  constexpr int RW = QS ? 2 * kWaves : kWaves;
+  constexpr int UNITS = 2 * QB, UPW = (UNITS + RW - 1) / RW;
   // One LDS object per ring slot: the compiler's wait for a slot's DMA then covers
   // that slot only, not the refills in flight for the others.
   __shared__ __attribute__((aligned(16))) char slot0[TILE];
@@ -317,10 +329,13 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
   // w: the feature slice this wave serves; helper: a warp-specialized helper wave
-  // (helpers branch off into a loop of their own before the first key tile).
-  const int w = WS ? (wv & (kWaves - 1)) : wv;
+  // (helpers branch off into a loop of their own before the first key tile); h:
+  // the query half of a query-split wave, whose query blocks are qb0 .. qb0+QBW-1.
+  const int w = (WS || QS) ? (wv & (kWaves - 1)) : wv;
   const bool helper = WS && wv >= kWaves;
   const bool do_mma = !helper;
+  const int h = QS ? (wv >> 2) : 0;
+  const int qb0 = h * QBW;
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
   const int n_qt = (C + BM - 1) / BM;
   const int b = (int)blockIdx.x % B;
@@ -371,7 +386,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   constexpr int P = Gm::P, RPP = Gm::RPP;
   // The DMA lane offsets stay in registers unless the variant's registers are
   // full (BM = 64 with 768-feature rows), where they are recomputed per tile.
-  constexpr bool KOF_LIVE = QB * NK < 24;
+  constexpr bool KOF_LIVE = !QS && QB * NK < 24;
   uint32_t kof_live[P];
   if constexpr (KOF_LIVE) {
 #pragma unroll
@@ -394,16 +409,18 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     return *reinterpret_cast<const u32x4*>(base + a1[s % (G / 4)] + 16 * (16 * row16 * CPRP + G * (s / (G / 4))));
   };
 
-  // Reduction units: unit u = w + 4j -> (query block u/2, key half u%2). Waves
-  // with fewer real units than UPW run a copy of unit 0 whose results go to the
-  // sink rows, so every wave executes the same branch-free code.
+  // Reduction units: unit u = r + RW j -> (query block u/2, key half u%2), r the
+  // wave's rank among the RW reducing waves. Waves with fewer real units than UPW
+  // run a copy of unit 0 whose results go to the sink rows, so every wave executes
+  // the same branch-free code.
+  const int rr = QS ? wv : w;
   int uq[UPW], uk[UPW], pq[UPW];
   float ud[UPW];
   uint32_t voff[UPW];
 #pragma unroll
   for (int j = 0; j < UPW; ++j) {
-    const bool real = (UNITS % kWaves == 0) || (w + kWaves * j < UNITS);
-    const int u = real ? w + kWaves * j : 0;
+    const bool real = (UNITS % RW == 0) || (rr + RW * j < UNITS);
+    const int u = real ? rr + RW * j : 0;
     uq[j] = u >> 1;
     uk[j] = u & 1;
     pq[j] = real ? uq[j] : QB;
@@ -444,23 +461,45 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     for (int kb = 0; kb < 2; ++kb)
       zv[I][kb] = ld8(rows_rsrc(vb, t * kBN + 16 * kb, live ? valid_rows : 0, 1u, 1u), (uint32_t)li);
   };
+  // This wave's share of a key tile's copies: all KDMA, or (query split) the half
+  // jj + h KD of them, KD = P, so the lane offsets are indexed by jj alone.
+  // Query split: the copies go out whether or not there is a tile to fetch (`live`;
+  // otherwise through an empty resource, writing zeros into the free slot), so that
+  // every iteration issues the same number of copies and the waits that order them
+  // for the partner wave can count them (see wait_next_tile).
+  constexpr bool UNCOND = QS;
+  // A refilled tile's validity bytes: loaded after its copies by the 4-wave variants
+  // (they are then live for less of the iteration, which the 64-row variants'
+  // registers need), before them by the others (the query-split waits count the
+  // copies as the newest loads).
+  constexpr bool VALID_LATE = !QS && !WS;
+  auto fetch_key_share = [&](int t, char* dst, int jj, const uint32_t (&kof)[P], bool live) {
+    if constexpr (QS)
+      dma16(rows_rsrc(zb, t * kBN + RPP * h, live ? C : 0, zstride, row_bytes), dst + 1024 * (h * KD + jj), kof[jj]);
+    else
+      fetch_key_part(t, dst, jj, kof);
+  };
   auto fetch_keys = [&](int t, auto slot) {
     uint32_t kof[P];
     key_offsets(kof);
 #pragma unroll
-    for (int j = 0; j < KDMA; ++j) fetch_key_part(t, slot_base(slot), j, kof);
+    for (int j = 0; j < KD; ++j) fetch_key_share(t, slot_base(slot), j, kof, true);
     fetch_valid(t, slot);
   };
   // BM rows (`stride` bytes apart) of a batch item from row q0 into a row region
   // (prologue: the queries; tail: the gate).
+  // (Query split: the wave's half of the rows, copies h JR .. h JR + JR - 1.)
+  constexpr int JR = BM * CPRP / 64 / (QS ? 2 : 1);  // copies of a wave's row share
   auto fetch_rows = [&](const char* src, uint32_t stride, auto region) {
     uint32_t kof[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane, stride);
 #pragma unroll
-    for (int j = 0; j < BM * CPRP / 64; ++j)
+    for (int jj = 0; jj < JR; ++jj) {
+      const int j = h * JR + jj;  // JR is a multiple of P: j % P == jj % P
       dma16(rows_rsrc(src, q0 + RPP * (j / P), C, stride, row_bytes), region(j / KDMA) + 1024 * (j % KDMA),
-            kof[j % P]);
+            kof[jj % P]);
+    }
   };
   // V entries of tile k0 for this wave's units (raw 16-bit words, two per dword): the
   // lane's four keys are adjacent, so with an even context one dword-aligned 8-byte
@@ -505,46 +544,51 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   constexpr int kTouchLead = 3;
   const bool gate_fits = (uint64_t)B * (uint64_t)C * row_bytes <= (8ull << 20);
   const int touch_t = gate_fits ? 0 : nkt - kTouchLead;  // the iteration that touches; < 1: here
-  auto touch_gate = [&]() {  // by the 256 lanes of the product waves
+  constexpr int kTouchLanes = QS ? Gm::THREADS : kThreads;  // lanes of the touching waves
+  auto touch_gate = [&]() {
     const rsrc_t r = rows_rsrc(gb, q0, min(C, q0 + BM), gstride, row_bytes);
-    constexpr int kLines = 4 * 32 * NK * 2 / 128;                          // 128-byte lines per row
-    constexpr int kTouches = (BM * kLines + kThreads - 1) / kThreads;     // lines over 256 lanes
+    constexpr int kLines = 4 * 32 * NK * 2 / 128;                              // 128-byte lines per row
+    constexpr int kTouches = (BM * kLines + kTouchLanes - 1) / kTouchLanes;  // lines over the lanes
 #pragma unroll
     for (int i = 0; i < kTouches; ++i) {
-      const uint32_t line = (uint32_t)(i * kThreads + tid), c = line % kLines;
+      const uint32_t line = (uint32_t)(i * kTouchLanes + tid), c = line % kLines;
       dma4(r, touch_sink, c * 128u < row_bytes ? (line / kLines) * gstride + c * 128u : kNowhere);
     }
   };
-  if (do_mma && has_gate && touch_t < 1) touch_gate();
-  u32x4 qf[QB][NK];
+  // (Query split: after the first barrier, which waits for every copy before it.)
+  if (!QS && do_mma && has_gate && touch_t < 1) touch_gate();
+  // Query fragments of this wave's query blocks (local index qb: block qb0 + qb).
+  u32x4 qf[QBW][NK];
   if (do_mma) {
-  uint32_t qv[QB];
+  uint32_t qv[QBW];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u, 1u), (uint32_t)li);
+  for (int qb = 0; qb < QBW; ++qb)
+    qv[qb] = ld8(rows_rsrc(vb, q0 + 16 * (qb0 + qb), valid_rows, 1u, 1u), (uint32_t)li);
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const bool ok = (16 * qb + li < C - q0) && ((qv[qb] | or_valid) != 0u);
+  for (int qb = 0; qb < QBW; ++qb) {
+    const int qg = qb0 + qb;
+    const bool ok = (16 * qg + li < C - q0) && ((qv[qb] | or_valid) != 0u);
     float ss = 0.f;
 #pragma unroll
     for (int s = 0; s < NK; ++s) {
-      const u32x4 x = frag_a(qrows_base(qb >> 1), qb & 1, s);
+      const u32x4 x = frag_a(qrows_base(qg >> 1), qg & 1, s);
       qf[qb][s] = ok ? x : zero4();  // select, so NaN in padded rows never enters
       ss = Ops<T16>::sumsq(qf[qb][s], ss);
     }
     ss = sum_over_groups(ss);
-    if (lg == 0) sm.nq[w][16 * qb + li] = ok ? ss : -1.f;
+    if (lg == 0) sm.nq[w][16 * qg + li] = ok ? ss : -1.f;
   }
   }
 
-  f32x4 oacc[NT][QB];
+  f32x4 oacc[NT][QBW];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) oacc[t][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int qb = 0; qb < QBW; ++qb) oacc[t][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float den[UPW];
 #pragma unroll
   for (int j = 0; j < UPW; ++j) den[j] = 0.f;
-  f32x4 sacc[2][QB];
+  f32x4 sacc[2][QBW];
   u32x2 vv[UPW];
   u32x4 ztr[NT];  // transposed mixing operands of the previous tile
 
@@ -567,8 +611,11 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // [0, KA), C the rest), while the 64-row variants, whose registers are full, keep
   // it in A, one DMA per step. A issues DMAs [0, JE). The DMAs sit under their own
   // uniform branches, so the MFMA code is not duplicated.
-  constexpr bool SPLIT = BM <= 32;
-  constexpr int KA = SPLIT ? (KDMA + 1) / 2 : KDMA;
+  // (Query split: the 64-row variants take this order too. Their halved
+  // accumulators leave room for the mixing operands across the barrier, and the other
+  // order would let one wave's refill overwrite rows its partner is still reading.)
+  constexpr bool SPLIT = BM <= 32 || QS;
+  constexpr int KA = SPLIT ? (KD + 1) / 2 : KD;
   constexpr int SP = SPLIT ? 2 : 1;  // MFMA steps per DMA in A
   auto stage_a = [&](int t, auto slot, int tf, auto fslot, bool refill, auto je) {
     constexpr int I = decltype(slot)::value;
@@ -597,24 +644,25 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     for (int kb = 0; kb < 2; ++kb) {
       const bool ok = (16 * kb + li < C - k0) && ((zv[I][kb] | or_valid) != 0u);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int qb = 0; qb < QBW; ++qb) sacc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < NK; ++s) {
         const u32x4 a = frag_a(base, kb, s);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
+        for (int qb = 0; qb < QBW; ++qb) sacc[kb][qb] = Ops<T16>::mfma32(a, qf[qb][s], sacc[kb][qb]);
         ss = Ops<T16>::sumsq(a, ss);
         const int step = kb * NK + s;
-        if (step % SP == 0 && step / SP < JE && refill) fetch_key_part(tf, slot_base(fslot), step / SP, kof);
+        if (step % SP == 0 && step / SP < JE && (UNCOND || refill))
+          fetch_key_share(tf, slot_base(fslot), step / SP, kof, refill);
       }
       ss = sum_over_groups(ss);
       nkey[kb] = ok ? ss : -1.f;
     }
-    if (refill) {
+    if (UNCOND || refill) {
 #pragma unroll
-      for (int j = (2 * NK + SP - 1) / SP; j < JE; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
-      if constexpr (JE == KDMA) fetch_valid(tf, fslot);
+      for (int j = (2 * NK + SP - 1) / SP; j < JE; ++j) fetch_key_share(tf, slot_base(fslot), j, kof, refill);
+      if constexpr (VALID_LATE && JE == KD) fetch_valid(tf, fslot);
     }
     // Lane groups 0 / 1 write the two key halves (groups 2 / 3 repeat them).
     sm.nxp[w][16 * (lg & 1) + li] = (lg & 1) ? nkey[1] : nkey[0];
@@ -656,21 +704,22 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     constexpr bool FETCH = SPLIT && decltype(fetch)::value;
     uint32_t kof[P];
     if constexpr (FETCH) key_offsets(kof);
-    u32x4 pf[QB];
+    u32x4 pf[QBW];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) pf[qb] = px[qb][lane];
+    for (int qb = 0; qb < QBW; ++qb) pf[qb] = px[qb0 + qb][lane];
 #pragma unroll
     for (int t2 = 0; t2 < NT; ++t2)
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
+      for (int qb = 0; qb < QBW; ++qb) {
         oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pf[qb], oacc[t2][qb]);
-        const int m = t2 * QB + qb;
-        if (m % 2 == 0 && KA + m / 2 < KDMA && FETCH && refill) fetch_key_part(tf, slot_base(fslot), KA + m / 2, kof);
+        const int m = t2 * QBW + qb;
+        if (m % 2 == 0 && KA + m / 2 < KD && FETCH && (UNCOND || refill))
+          fetch_key_share(tf, slot_base(fslot), KA + m / 2, kof, refill);
       }
-    if (FETCH && refill) {
+    if (FETCH && (UNCOND || refill)) {
 #pragma unroll
-      for (int j = KA + (NT * QB + 1) / 2; j < KDMA; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
-      fetch_valid(tf, fslot);
+      for (int j = KA + (NT * QBW + 1) / 2; j < KD; ++j) fetch_key_share(tf, slot_base(fslot), j, kof, refill);
+      if constexpr (VALID_LATE) fetch_valid(tf, fslot);
     }
   };
 
@@ -682,7 +731,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) sx[w][kb][qb][lane] = sacc[kb][qb];
+        for (int qb = 0; qb < QBW; ++qb) sx[w][kb][qb0 + qb][lane] = sacc[kb][qb];
     }
     if constexpr (decltype(red)::value) {
       const int k = lane & (kBN - 1);
@@ -710,11 +759,34 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
   // s_waitcnt encodings (gfx9: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at
   // their maxima, i.e. not waited for).
-  static_assert(KDMA < 64, "vmcnt holds 6 bits");
+  static_assert(KDMA + 2 < 64, "vmcnt holds 6 bits");
   auto wait_all = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
-  // All but the newest KDMA vector-memory operations retired (they return in issue
-  // order): the refill just issued may stay in flight.
-  auto wait_keep_refill = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70 | (KDMA & 15) | ((KDMA >> 4) << 14)); };
+  // All but the newest N vector-memory operations retired (they return in issue order).
+  auto wait_keep = [&](auto n) {
+    constexpr int N = decltype(n)::value;
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+  };
+  // The refill just issued (KDMA copies) may stay in flight.
+  auto wait_keep_refill = [&]() { wait_keep(IC<KDMA>{}); };
+  // Query split: each wave of a slice copies half of a key tile's rows and reads them
+  // all, so a wave's copies are ordered before its partner's reads by its own wait and
+  // a barrier. Before the barrier that closes iteration t, key tile t+1 has landed:
+  // with two slots it is this iteration's refill (all of it retires); with three it
+  // is the previous one, and this iteration's stays in flight: its KD copies, which
+  // every iteration issues (see fetch_key_share) after its other loads (the tile's
+  // validity bytes go out first), and which come after everything of the previous
+  // iteration (nothing moves across a barrier). Anything of this iteration issued
+  // after them only makes the wait retire more. After the last iteration everything
+  // retires: the tail's gate rows then land in slots that the partner's last (empty)
+  // copies also write.
+  auto wait_next_tile = [&](bool last) {
+    if constexpr (R == 3) {
+      wait_keep(IC<KD>{});
+      if (last) wait_all();
+    } else {
+      wait_all();
+    }
+  };
 
   // t = 0: A only (with the whole fetch of the last tile of the ring's first round);
   // the query norms, A(0)'s publication and tile 0's mixing operands. The query rows
@@ -782,13 +854,20 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // From here on: the product waves (all waves without warp specialization).
   constexpr bool RED = !WS;
   using RT = std::integral_constant<bool, RED>;
+  if constexpr (QS) {
+    // Key tile 0 (and 1) from both waves of the slice; the partner's query reads done
+    // before this wave's refill overwrites slot R-1.
+    wait_all();
+    lds_barrier();
+    if (has_gate && touch_t < 1) touch_gate();
+  }
   if constexpr (RED) load_v(0, vv);
   wait_lds_reads();
+  if constexpr (!VALID_LATE) fetch_valid(R - 1, IC<R - 1>{}, R - 1 < nkt);
   if constexpr (WS) {
-    fetch_valid(R - 1, IC<R - 1>{}, R - 1 < nkt);
     stage_a(0, IC<0>{}, 0, IC<R - 1>{}, false, IC<0>{});
   } else {
-    stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KDMA>{});
+    stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KD>{});
   }
   lds_barrier();
   if (tid < BM) {
@@ -800,6 +879,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   }
   publish(TT{}, RT{});
   if constexpr (SPLIT) stage_t(IC<0>{});
+  if constexpr (QS) wait_next_tile(nkt == 1);
   lds_barrier();
   // Steady state, unrolled by R so that every slot index is a constant. Iteration
   // t runs B(t-1), then A(t); then C(t-1) and A(t)'s publication, and refills tile
@@ -827,6 +907,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     // The V words B consumes were loaded an iteration ago.
     stage_b(t - 1);
     if (has_gate && t == touch_t) touch_gate();
+    if constexpr (!VALID_LATE) fetch_valid(t + R - 1, IC<PREV>{}, refill);
     if constexpr (!SPLIT) wait_lds_reads();  // the refill overwrites what T read
     stage_a(t, cur, t + R - 1, IC<PREV>{}, refill, IC<KA>{});
     lds_barrier();
@@ -838,6 +919,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
       __builtin_amdgcn_sched_barrier(0);
       stage_t(cur);
     }
+    if constexpr (QS) wait_next_tile(t + 1 == nkt);
     lds_barrier();
   };
   run_loop(iteration);
@@ -856,7 +938,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // The epilogue's bias words and validity bytes, now that the query fragments are
   // dead: their latency hides behind the last reduction and mixing product.
   u32x2 bw[NT];
-  uint32_t qv2[QB];
+  uint32_t qv2[QBW];
   {
     const rsrc_t rbias = make_rsrc(has_bias ? p.bias : p.z, has_bias ? row_bytes : 0u);
 #pragma unroll
@@ -865,13 +947,14 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
       bw[t2] = ld64(rbias, (FULL || f < D) ? (uint32_t)f * 2u : kNowhere);
     }
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * qb, valid_rows, 1u, 1u), (uint32_t)li);
+    for (int qb = 0; qb < QBW; ++qb)
+      qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * (qb0 + qb), valid_rows, 1u, 1u), (uint32_t)li);
   }
   if constexpr (RED) stage_b(nkt - 1);
   lds_barrier();
   stage_c(0, IC<0>{}, false, FF{});
 
-  // ---- epilogue: lane holds query 16*qb+li, features fw+16t+4*lg .. +3 ------------------
+  // ---- epilogue: lane holds query 16*(qb0+qb)+li, features fw+16t+4*lg .. +3 ----------
   uint32_t a3[G / 2];
 #pragma unroll
   for (int m = 0; m < G / 2; ++m)
@@ -879,7 +962,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   auto efrag = [&](int qb, int t2) -> char* {
     return erows_base(qb >> 1) + a3[t2 % (G / 2)] + 16 * (16 * (qb & 1) * CPRP + G * (t2 / (G / 2)));
   };
-  float rden[QB];
+  float rden[QBW];
   if (p.normalize) {
     if constexpr (RED) {
 #pragma unroll
@@ -896,10 +979,10 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
     lds_barrier();
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rden[qb] = sm.dq[16 * qb + li];
+    for (int qb = 0; qb < QBW; ++qb) rden[qb] = sm.dq[16 * (qb0 + qb) + li];
   } else {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) rden[qb] = 1.f;
+    for (int qb = 0; qb < QBW; ++qb) rden[qb] = 1.f;
   }
   const uint32_t one2 = Ops<T16>::kOne | (Ops<T16>::kOne << 16);
   // The result goes back into this wave's gate slots, then out in 16-byte runs. The
@@ -916,14 +999,14 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   auto finish = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < QBW; ++qb) {
       const bool qok = (qv2[qb] | or_valid) != 0u;
 #pragma unroll
       for (int tb = 0; tb < NT; tb += GB) {
         u32x2 gw[GB];
 #pragma unroll
         for (int i = 0; i < GB; ++i)
-          gw[i] = has_gate ? *reinterpret_cast<const u32x2*>(efrag(qb, tb + i)) : u32x2{one2, one2};
+          gw[i] = has_gate ? *reinterpret_cast<const u32x2*>(efrag(qb0 + qb, tb + i)) : u32x2{one2, one2};
 #pragma unroll
         for (int i = 0; i < GB; ++i) {
           const int t2 = tb + i;
@@ -937,7 +1020,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
             x *= (k & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
             y[k] = qok ? x : 0.f;
           }
-          *reinterpret_cast<u32x2*>(efrag(qb, t2)) = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
+          *reinterpret_cast<u32x2*>(efrag(qb0 + qb, t2)) = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
         }
       }
     }
@@ -949,15 +1032,17 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     case AVEY_ACT_GELU: finish(std::integral_constant<int, AVEY_ACT_GELU>{}); break;
     default: finish(std::integral_constant<int, AVEY_ACT_IDENTITY>{}); break;
   }
-  // Rows past the context fall outside the resources and are dropped.
+  // Rows past the context fall outside the resources and are dropped. A wave writes
+  // out the rows it wrote above (query split: its half, as in fetch_rows).
   const char* ob = (const char*)p.out + (int64_t)b * C * row_bytes;
   uint32_t kof[P];
 #pragma unroll
   for (int j = 0; j < P; ++j) kof[j] = goff(64 * j + lane, row_bytes);
 #pragma unroll
-  for (int j = 0; j < BM * CPRP / 64; ++j) {
+  for (int jj = 0; jj < JR; ++jj) {
+    const int j = h * JR + jj;
     const u32x4 v = *reinterpret_cast<const u32x4*>(erows_base(j / KDMA) + 1024 * (j % KDMA) + 16 * lane);
-    st128(v, rows_rsrc(ob, q0 + RPP * (j / P), C, row_bytes, row_bytes), kof[j % P]);
+    st128(v, rows_rsrc(ob, q0 + RPP * (j / P), C, row_bytes, row_bytes), kof[jj % P]);
   }
 }
 

@@ -23,11 +23,18 @@ mixing operands (``ds_read_b64_tr_b16``) and the epilogue's gate words
   copy at a key read; after it, no prologue copy at any key or mixing read;
 * ring refills: a copy in flight at a key read has passed at most 2 (R - 2)
   barriers (an older one filled the slot being read); at a mixing read at most
-  2 (R - 2) + 1 for the 16/32-row variants (they read the mixing operands at the
-  end of the tile's own iteration) or 2 (R - 1) for the 64-row variants (at the
-  start of the next);
+  2 (R - 2) + 1 where the mixing operands are read at the end of the tile's own
+  iteration (all but the 4-wave 64-row variants), else 2 (R - 1) (at the start
+  of the next);
 * gate reads: nothing in flight but the 4-byte cache-line touches, whose
   landing place is never read.
+
+In the query-split variants (32 and 64 rows, see query_split) the two waves of a feature slice
+each copy half of a key tile's rows and both read all of them, so a copy is
+visible to the partner only once it retired before a barrier the partner then
+passed. For those, a copy retired by a wait stays "pending" (counted as in
+flight at key, mixing and prologue key reads) until the next barrier; the query
+and gate rows a wave reads are its own copies, for which its own wait suffices.
 
 Branch correlations are ignored (every path through the graph counts), so the
 check can over-report but not miss a path. The 8-wave variants' helper waves
@@ -40,13 +47,20 @@ import re
 from collections import defaultdict
 
 CAP_LOADS, CAP_BARRIERS = 64, 9
+PENDING = 10 ** 6  # load count of a retired copy not yet ordered by a barrier (query split)
 _KERNEL = re.compile(r'^(_ZN4avey16fused_fwd_kernelI\w+):', re.M)
 _SHAPE = re.compile(r'fused_fwd_kernelI\w+?Li(\d+)ELi(\d+)ELb(\d)E')
 
 
+def query_split(bm, nk):
+    """Whether the (BM, NK) variant splits its query blocks over two waves per slice
+    (the kernel's fused_query_split)."""
+    return (bm == 32 and nk <= 6) or (bm == 64 and nk <= 4)
+
+
 def ring(bm, nk):
-    """(R, copies per key tile, copies for the query rows) of a (BM, NK) variant,
-    as the kernel's LDS geometry fixes them."""
+    """(R, copies per key tile, copies for the query rows) one wave issues in a
+    (BM, NK) variant, as the kernel's LDS geometry fixes them (query split: half)."""
     cpr = 4 * nk
     cprp = (cpr + 7) // 8 * 8
     tile = 4 * 32 * cprp * 16
@@ -55,7 +69,8 @@ def ring(bm, nk):
     ovf = tile if (bm > 32 and tile > sx + px) else sx + px
     small = 4 * (4 * 32 + 32 + 4 * bm + bm + (qb + 1) * 2 * 4 * 16 + bm)
     r = 3 if 3 * tile + ovf + small <= 160 * 1024 else 2
-    return r, 32 * cprp // 64, bm * cprp // 64
+    share = 2 if query_split(bm, nk) else 1
+    return r, 32 * cprp // 64 // share, bm * cprp // 64 // share
 
 
 def kernels(asm_text):
@@ -104,7 +119,8 @@ def _blocks(lines):
 
 
 def _is_vmem_load(t):
-    return t.startswith(('buffer_load', 'global_load', 'flat_load'))
+    # (Stores count in vmcnt as well; leaving them out only makes the check stricter.)
+    return t.startswith(('buffer_load', 'global_load', 'flat_load', 'scratch_load'))
 
 
 def _is_copy(t):
@@ -113,6 +129,13 @@ def _is_copy(t):
 
 def _is_touch(t):
     return t.startswith('buffer_load_dword ') and t.endswith(' lds')
+
+
+def _front(pairs):
+    out = []
+    for q in pairs:
+        out, _ = _add(out, q)
+    return out
 
 
 def _add(front, pair):
@@ -159,7 +182,8 @@ def _role(flat, i):
 def check_kernel(lines, bm, nk):
     """Violations [(read, rule)] and per-role read counts of one kernel."""
     r, kdma, nq = ring(bm, nk)
-    split = bm <= 32
+    qs = query_split(bm, nk)
+    split = bm <= 32 or qs
     blocks, succ = _blocks(lines)
     order, gidx, flat, first_barrier = [], {}, [], None
     for k, (_, ins) in enumerate(blocks):
@@ -188,12 +212,17 @@ def check_kernel(lines, bm, nk):
             m = re.search(r'vmcnt\((\d+)\)', t) if t.startswith('s_waitcnt') else None
             if m:
                 n = int(m.group(1))
-                st = {s: [q for q in f if q[0] < n] for s, f in st.items()}
+                if qs:
+                    st = {s: _front([q if q[0] < n else (PENDING, q[1]) for q in f]) for s, f in st.items()}
+                else:
+                    st = {s: [q for q in f if q[0] < n] for s, f in st.items()}
                 st = {s: f for s, f in st.items() if f}
             elif t.startswith('s_barrier'):
-                st = {s: [(q[0], min(q[1] + 1, CAP_BARRIERS)) for q in f] for s, f in st.items()}
+                st = {s: [(q[0], min(q[1] + 1, CAP_BARRIERS)) for q in f if q[0] != PENDING] for s, f in st.items()}
+                st = {s: f for s, f in st.items() if f}
             elif _is_vmem_load(t):
-                st = {s: [(min(q[0] + 1, CAP_LOADS), q[1]) for q in f] for s, f in st.items()}
+                st = {s: [(q[0] if q[0] == PENDING else min(q[0] + 1, CAP_LOADS), q[1]) for q in f]
+                      for s, f in st.items()}
                 if _is_copy(t) and not _is_touch(t):
                     st[(k, p)] = [(0, 0)]
             elif t.startswith('ds_read'):
@@ -224,6 +253,10 @@ def check_kernel(lines, bm, nk):
             continue
         counts[role] += 1
         for s, front in st.items():
+            if role in ('G', 'Q'):  # the wave's own rows: pending copies have landed
+                front = [q for q in front if q[0] != PENDING]
+                if not front:
+                    continue
             bars = max(q[1] for q in front)
             why = None
             if role == 'G':

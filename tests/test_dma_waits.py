@@ -25,17 +25,21 @@ TOUCH = 'buffer_load_dword v1, s[0:3], 0 offen lds'
 LOAD = 'buffer_load_dwordx2 v[4:5], v1, s[0:3], 0 offen'
 
 
-def _bad(lines, bm=32, nk=8):
+def _bad(lines, bm=16, nk=8):
     bad, _ = dw.check_kernel(lines + ['s_endpgm'], bm, nk)
     return bad
 
 
 def test_ring_geometry():
-    # (R, copies per tile, copies for the query rows): C2's variant keeps three
-    # slots, 768-feature rows in the 32-row variant only two.
+    # (R, copies per key tile, copies for the query rows, per wave): C2's variant
+    # keeps three slots, 768-feature rows in the 32-row variant only two; the 32-
+    # and 64-row variants split the copies between the two waves of a slice.
     assert dw.ring(16, 6) == (3, 12, 6)
-    assert dw.ring(32, 6) == (2, 12, 12)
-    assert dw.ring(64, 4) == (3, 8, 16)
+    assert dw.ring(16, 8) == (2, 16, 8)
+    assert dw.ring(32, 6) == (2, 6, 6)
+    assert dw.ring(32, 8) == (2, 16, 16)
+    assert dw.ring(64, 4) == (3, 4, 8)
+    assert dw.ring(64, 6) == (2, 12, 24)
 
 
 def test_refill_read_without_wait_is_flagged():
@@ -77,10 +81,24 @@ def test_prologue_and_gate_rules():
 
 
 def test_mixing_read_rule():
-    # 32-row variants read tile t's mixing operands at the end of iteration t: its
-    # own refill (one barrier back) may be in flight, the previous one may not.
+    # Tile t's mixing operands are read at the end of iteration t: its own refill
+    # (one barrier back) may be in flight, the previous one may not.
     assert not _bad(['s_barrier', COPY, 's_barrier'] + MIX)
     assert _bad(['s_barrier', COPY, 's_barrier', 's_barrier'] + MIX)
+
+
+def test_query_split_needs_the_wait_before_the_barrier():
+    # Both waves of a slice read the rows each one copied: a wait after the barrier
+    # orders the copy for this wave only, not for its partner.
+    bm, nk = 32, 6
+    assert _bad(['s_barrier', COPY, 's_barrier', 's_waitcnt vmcnt(0)'] + KEY, bm, nk)
+    assert not _bad(['s_barrier', COPY, 's_waitcnt vmcnt(0)', 's_barrier'] + KEY, bm, nk)
+    assert _bad(['s_barrier', COPY, 's_barrier', 's_barrier', 's_waitcnt vmcnt(0)'] + MIX, bm, nk)
+    assert not _bad(['s_barrier', COPY, 's_barrier', 's_waitcnt vmcnt(0)', 's_barrier'] + MIX, bm, nk)
+    # A wave's own query and gate rows need only its own wait.
+    assert not _bad([COPY, 's_waitcnt vmcnt(0)'] + GATE, bm, nk)
+    _, kdma, nq = dw.ring(bm, nk)
+    assert not _bad([COPY] * (nq + kdma) + [f's_waitcnt vmcnt({kdma})'] + QUERY, bm, nk)
 
 
 def _compile(src, out_dir):
