@@ -125,7 +125,11 @@ Plan make_plan(const avey_fwd_args& a) {
     pl.kernel = 1;
     pl.bn = 32;
     pl.bd = 32 * nk;
-    int bm = nk <= 6 ? 64 : 32;
+    // Row block: 64 rows up to 192 features per slice (768-feature rows), halved
+    // while the grid would not cover the 256 CUs. Wider rows take the 16-row warp-
+    // specialized variant: the 32-row one for 1024-feature rows keeps 4 waves (its
+    // state does not fit 256 registers) and was 1.23x slower on B4 N2048 causal.
+    int bm = nk <= 6 ? 64 : 16;
     while (bm > 16 && cdiv(a.context, bm) * a.batch < 256) bm /= 2;
     pl.bm = bm;
     pl.threads = fused_threads(bm, nk);

@@ -1070,7 +1070,8 @@ hipError_t launch_fused_nk(const FwdParams& p, int nk, int64_t grid, hipStream_t
     case 4: return launch_fused_one<T16, BM, 4, STRIDED>(p, grid, s);
     case 6: return launch_fused_one<T16, BM, 6, STRIDED>(p, grid, s);
     case 8:
-      if constexpr (BM <= 32) return launch_fused_one<T16, BM, 8, STRIDED>(p, grid, s);
+      // 1024-feature rows take the 16-row variant only (the plan's choice for them).
+      if constexpr (BM == 16) return launch_fused_one<T16, BM, 8, STRIDED>(p, grid, s);
       return hipErrorInvalidConfiguration;
     default: return hipErrorInvalidConfiguration;
   }

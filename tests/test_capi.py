@@ -100,6 +100,14 @@ def test_static_tile_table():
     for shape in ((32, 512, 768), (4, 2048, 1024), (256, 128, 512)):
         q = _hip.plan(shape, torch.bfloat16, causal=False, normalize=True)
         assert q['kernel'] == 'fused_mfma' and q['grid'] >= 256
+    # Row blocks and threads per workgroup: 8 waves where a variant splits roles (16
+    # rows) or query blocks (32 / 64 rows whose state fits 256 registers), 4 where it
+    # needs 512 registers per lane.
+    for shape, causal, bm, threads in (((16, 256, 768), True, 16, 512), ((32, 512, 768), False, 64, 256),
+                                       ((4, 2048, 1024), True, 16, 512), ((256, 128, 512), False, 64, 512),
+                                       ((64, 128, 256), False, 32, 512)):
+        q = _hip.plan(shape, torch.bfloat16, causal=causal, normalize=True)
+        assert (q['block_m'], q['threads']) == (bm, threads), shape
     # Causal skipping visits about half the key tiles of the full traversal.
     full = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=False, normalize=False)
     half = _hip.plan((4, 2048, 1024), torch.bfloat16, causal=True, normalize=False)
