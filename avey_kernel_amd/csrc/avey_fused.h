@@ -520,13 +520,17 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
-  // In the 8-wave variants the helpers copy tile 1 (first thing in their program),
-  // so that the product waves reach the query norms and A(0) after issuing only the
-  // query rows and tile 0 (the copy queue is in issue order); the product waves still
-  // load tile 1's validity bytes, which they use.
+  // In the warp-specialized variants the helpers copy tiles 0 and 1 (first thing in
+  // their program; tile 0 is then ordered for the product waves by their wait and a
+  // barrier before A(0)), so that the product waves issue only the query rows and
+  // reach the query norms early; the product waves still load the tiles' validity
+  // bytes, which they use.
   if (do_mma) {
     fetch_rows((const char*)zb, zstride, qrows_base);
-    fetch_keys(0, IC<0>{});
+    if constexpr (WS)
+      fetch_valid(0, IC<0>{});
+    else
+      fetch_keys(0, IC<0>{});
     if constexpr (R == 3) {
       if (1 < nkt) {
         if constexpr (WS)
@@ -818,7 +822,14 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     if (helper) {
       // The helpers' program: the same barriers as the product waves', in order.
       constexpr int KH = KDMA / 2;
-      if (R == 3 && 1 < nkt) refill_part(1, IC<1>{}, IC<0>{}, IC<KDMA>{});  // tile 1 (see the prologue)
+      refill_part(0, IC<0>{}, IC<0>{}, IC<KDMA>{});  // tiles 0 and 1 (see the prologue)
+      if (R == 3 && 1 < nkt) {
+        refill_part(1, IC<1>{}, IC<0>{}, IC<KDMA>{});
+        wait_keep_refill();
+      } else {
+        wait_all();
+      }
+      lds_barrier();  // tile 0 has landed
       load_v(0, vv);
       lds_barrier();  // A(0) done, the query rows in slot R-1 consumed
       if (R - 1 < nkt) refill_part(R - 1, IC<R - 1>{}, IC<0>{}, IC<KDMA>{});
@@ -861,6 +872,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     lds_barrier();
     if (has_gate && touch_t < 1) touch_gate();
   }
+  if constexpr (WS) lds_barrier();  // the helpers' copy of tile 0
   if constexpr (RED) load_v(0, vv);
   wait_lds_reads();
   if constexpr (!VALID_LATE) fetch_valid(R - 1, IC<R - 1>{}, R - 1 < nkt);
