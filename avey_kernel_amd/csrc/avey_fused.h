@@ -829,12 +829,16 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
       } else {
         wait_all();
       }
-      lds_barrier();  // tile 0 has landed
+      lds_barrier();  // tile 0 has landed; the query rows in slot R-1 are consumed
       load_v(0, vv);
-      lds_barrier();  // A(0) done, the query rows in slot R-1 consumed
       if (R - 1 < nkt) refill_part(R - 1, IC<R - 1>{}, IC<0>{}, IC<KDMA>{});
+      lds_barrier();  // A(0) done
       publish(FF{}, TT{});
-      wait_all();
+      // Tile 1 lands before iteration 1; with three slots tile 2 may stay in flight.
+      if (R == 3 && R - 1 < nkt)
+        wait_keep_refill();
+      else
+        wait_all();
       lds_barrier();
       run_loop([&](int t, auto cur) {
         constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
