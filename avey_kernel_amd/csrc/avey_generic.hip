@@ -73,9 +73,66 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     rq[t] = q < C ? inv[q] : A(0);
   }
   auto row_ok = [&](int64_t r) { return r < C && (!vb || vb[r]); };
+  const bool small = D <= DC;  // one feature chunk (C1's shape)
 
   const int64_t nkt = key_tiles_for(qt, C, BQ, BK, p.causal != 0);
-  for (int64_t kt = 0; kt < nkt; ++kt) {
+  if (small) {
+    // The query rows are loaded once, a key tile's rows serve both the similarities
+    // and the mixing (BF == DC), and the next tile's rows, this thread's V entry and
+    // key inverse norm are loaded while the current tile is used, so a tile waits on
+    // no global-load round trip. Same arithmetic in the same order as below.
+    static_assert(BF == DC && BK * DC % 256 == 0, "key rows serve the mixing");
+    for (int e = t; e < BQ * DC; e += 256) {
+      const int r = e / DC, c = e % DC;
+      const int64_t q = q0 + r;
+      qs[r][c] = (c < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * p.zrs + c]) : A(0);
+    }
+    constexpr int KE = BK * DC / 256;  // key-row elements per thread
+    A kr[KE];
+    auto load_keys = [&](int64_t k0) {
+#pragma unroll
+      for (int i = 0; i < KE; ++i) {
+        const int e = t + 256 * i, r = e / DC, c = e % DC;
+        const int64_t k = k0 + r;
+        kr[i] = (c < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + c]) : A(0);
+      }
+    };
+    load_keys(0);
+    for (int64_t kt = 0; kt < nkt; ++kt) {
+      const int64_t k0 = kt * BK;
+      const int64_t q = q0 + si, k = k0 + sj;
+      const bool allowed = row_ok(q) && row_ok(k) && (!p.causal || k <= q);
+      const A ik = allowed ? inv[k] : A(0);
+      const A vv = (allowed && vw) ? Elem<T>::to_acc(vw[q * C + k]) : A(1);
+      __syncthreads();  // the previous tile's reads of ks and ss are done
+#pragma unroll
+      for (int i = 0; i < KE; ++i) ks[(t + 256 * i) / DC][(t + 256 * i) % DC] = kr[i];
+      if (kt + 1 < nkt) load_keys(k0 + BK);
+      __syncthreads();
+      A s = A(0);
+#pragma unroll 8
+      for (int c = 0; c < DC; ++c) s += qs[si][c] * ks[sj][c];
+      if (allowed) {
+        s = s * rq[si] * ik;
+        if (vw) s *= vv;
+      } else {
+        s = A(0);
+      }
+      ss[si][sj] = s;
+      __syncthreads();
+      if (p.normalize && t < BQ) {
+        A d = A(0);
+        for (int j = 0; j < BK; ++j) d += ss[t][j];
+        den_s[t] += d;
+      }
+#pragma unroll 4
+      for (int j = 0; j < BK; ++j) {
+        const A sv = ss[oi][j];
+        for (int u = 0; u < 4; ++u) acc[u] += sv * ks[j][of + u];
+      }
+    }
+  }
+  for (int64_t kt = 0; kt < (small ? 0 : nkt); ++kt) {
     const int64_t k0 = kt * BK;
     A s = A(0);
     for (int64_t d0 = 0; d0 < D; d0 += DC) {
