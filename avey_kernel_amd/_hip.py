@@ -60,6 +60,7 @@ EXPORTS = {
     'avey_device_supported': (ctypes.c_int, [ctypes.c_int]),
     'avey_status_string': (ctypes.c_char_p, [ctypes.c_int]),
     'avey_abi_version': (ctypes.c_int, []),
+    'avey_debug_poison_lds': (ctypes.c_int, [ctypes.c_void_p]),
 }
 ABI_VERSION = 2
 

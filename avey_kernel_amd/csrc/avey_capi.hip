@@ -100,10 +100,10 @@ bool device_ok(int dev) {
 // The static tile table (replaces the reference's runtime autotuner,
 // avey_kernels/_triton.py:131-150). For the fused kernel:
 //   * slice width DS = 32 * ceil(D / 128) features per wave (4 waves cover D);
-//   * BM = 64 query rows while the double-buffered key slices and the partial
-//     similarity tiles fit the 160 KB of LDS (DS <= 192), else 32;
+//   * BM = 64 query rows up to DS = 192 (the key-slice ring and the partial
+//     similarity tiles fit the 160 KB of LDS), else 16;
 //   * BM halves (down to 16) while the grid would leave CUs of the 256 idle;
-//   * the 16-row variants run 8 waves (warp-specialized), the others 4.
+//   * waves per workgroup as fused_threads (avey_common.h) gives them.
 // The fused kernel addresses memory with 16-byte row chunks and 32-bit buffer
 // offsets, so it also needs D % 8 == 0, 16-byte aligned z_tr / z_tl / out, row
 // and batch strides of z_tr / z_tl that are multiples of 8 elements, an 8-byte
@@ -159,7 +159,24 @@ Plan make_plan(const avey_fwd_args& a) {
 
 using namespace avey;
 
+namespace {
+// Test helper: fills a workgroup's whole LDS (160 KB) with words that are NaN both
+// as fp32 and as two bf16 / fp16 halves. A grid of 4 workgroups per CU, one at a
+// time (the LDS holds one), leaves every CU's LDS poisoned.
+constexpr int kPoisonWords = 160 * 1024 / 4;
+__global__ __launch_bounds__(1024) void poison_lds_kernel() {
+  __shared__ uint32_t buf[kPoisonWords];
+  volatile uint32_t* v = buf;
+  for (int i = threadIdx.x; i < kPoisonWords; i += 1024) v[i] = 0x7fc07fc0u;
+}
+}  // namespace
+
 extern "C" {
+
+int avey_debug_poison_lds(void* stream) {
+  poison_lds_kernel<<<dim3(1024), dim3(1024), 0, (hipStream_t)stream>>>();
+  return (int)hipGetLastError();
+}
 
 int avey_abi_version(void) { return AVEY_ABI_VERSION; }
 

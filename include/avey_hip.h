@@ -137,6 +137,12 @@ int avey_device_supported(int device);
 const char* avey_status_string(int status);
 int avey_abi_version(void);
 
+/* Test helper, no reference counterpart: fills the LDS of every CU with NaN bit
+ * patterns (fp32 and 16-bit alike) on `stream` (a hipStream_t; NULL: the null
+ * stream), so that a test can show a kernel's results do not depend on LDS it did
+ * not write. Returns a HIP status (0 on success). */
+int avey_debug_poison_lds(void* stream);
+
 #ifdef __cplusplus
 }
 #endif

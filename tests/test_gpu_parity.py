@@ -14,6 +14,7 @@ size, size-independent properties (bitwise determinism, causal rows blind to
 the future) and HIP-graph replay.
 """
 
+import ctypes
 import os
 
 import numpy as np
@@ -437,3 +438,40 @@ def test_every_fused_variant_matches_oracle(bm, d):
         _assert_close(out, want, torch.bfloat16, f'BM{bm} D{d} {label}', cond)
         if c['valid'] is not None:
             assert torch.all(out[~validd] == 0), f'BM{bm} D{d} {label}: padded rows not zero'
+
+
+# A kernel that reads LDS it never wrote (a padding chunk fed to an MFMA, a partial
+# read before its barrier) gives results that depend on what ran before on the CU.
+# The same call after every CU's LDS was filled with NaN bit patterns must give the
+# same bits as after a warm-up call of its own. Every fused variant, and both generic
+# kernel paths.
+_POISON_CASES = [(bm, d, torch.bfloat16) for bm, d in _VARIANTS] + [(16, 64, torch.float32),
+                                                                    (16, 200, torch.float32)]
+
+
+@pytest.mark.parametrize('bm,d,dtype', _POISON_CASES, ids=lambda x: str(x))
+def test_results_do_not_depend_on_stale_lds(bm, d, dtype):
+    lib = _hip.load()
+    batch, context = _BM_SHAPES[bm]
+    plan = _hip.plan((batch, context, d), dtype, causal=True, normalize=False)
+    if dtype == torch.bfloat16:
+        assert plan['kernel'] == 'fused_mfma' and plan['block_m'] == bm, plan
+    g = torch.Generator().manual_seed(bm * 7 + d)
+    z = torch.randn(batch, context, d, generator=g).to(DEV, dtype)
+    gate = torch.randn(batch, context, d, generator=g).to(DEV, dtype)
+    bias = (torch.randn(d, generator=g) * 0.1).to(DEV, dtype)
+    v = ((torch.rand(context, context, generator=g) * 2 - 1) / context ** 0.5).to(DEV, dtype)
+    lengths = torch.randint(context // 2, context + 1, (batch,), generator=g)
+    valid = (torch.arange(context)[None, :] < lengths[:, None]).to(DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for label, c in (('avey causal', dict(v=v, causal=True, normalize=False, valid=None, eps=1e-6, act='silu')),
+                     ('avey_b padded', dict(v=None, causal=False, normalize=True, valid=valid, eps=0.25, act='gelu'))):
+        args = (z, c['v'], gate, bias, c['valid'])
+        kw = dict(eps=c['eps'], causal=c['causal'], normalize=c['normalize'], act=c['act'])
+        _fused(*args, **kw)
+        warm = _fused(*args, **kw)
+        assert lib.avey_debug_poison_lds(ctypes.c_void_p(stream)) == 0
+        cold = _fused(*args, **kw)
+        torch.cuda.synchronize()
+        assert not torch.isnan(warm).any(), (bm, d, label)
+        assert torch.equal(cold, warm), (bm, d, label, (cold.float() - warm.float()).abs().nan_to_num(1e9).max())
