@@ -748,9 +748,11 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
 
   // ---- warp-specialized refill: a helper copies key tile tf into its slice of slot F,
   // copies [j0, j1) of KDMA. Issuing them is throttled by the CU's memory pipe (about
-  // 50 cycles per copy with four helpers issuing), so a steady-state iteration splits
-  // them: the first half after the reduction (the product waves run A meanwhile), the
-  // second after the key reciprocals (they run C and T). The product waves cannot
+  // 50 cycles per copy with four helpers issuing), so with three slots a steady-state
+  // iteration splits them: the first half after the reduction (the product waves run
+  // A meanwhile), the second after the key reciprocals (they run C and T); with two
+  // slots all go out after the reduction, as they must land within the iteration.
+  // The product waves cannot
   // wait for another wave's copies: the helper's wait and the next barrier are what
   // orders their reads after a copy. With three slots a refill is read two barriers
   // pairs later, so the wait at an iteration's end retires the previous iteration's
@@ -821,7 +823,9 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   if constexpr (WS) {
     if (helper) {
       // The helpers' program: the same barriers as the product waves', in order.
-      constexpr int KH = KDMA / 2;
+      // Copies issued before the reduction's barrier. With two slots the refill must
+      // land by the end of its own iteration, so all of it goes out early.
+      constexpr int KH = R == 2 ? KDMA : KDMA / 2;
       refill_part(0, IC<0>{}, IC<0>{}, IC<KDMA>{});  // tiles 0 and 1 (see the prologue)
       if (R == 3 && 1 < nkt) {
         refill_part(1, IC<1>{}, IC<0>{}, IC<KDMA>{});
