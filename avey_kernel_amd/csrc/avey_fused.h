@@ -1,9 +1,9 @@
 // Fused forward contextualizer for bf16 / fp16 on gfx950 MFMA.
 //
-// One workgroup (4 waves, one per SIMD) owns BM query rows of one batch item and
-// streams key tiles of BN = 32 rows over them. The feature axis is split four
-// ways: wave w owns the slice [w*DS, (w+1)*DS) for every product, so the 16-byte
-// row chunks it loads feed only itself. Per key tile t there are three stages:
+// One workgroup owns BM query rows of one batch item and streams key tiles of
+// BN = 32 rows over them. The feature axis is split four ways: feature slice w,
+// [w*DS, (w+1)*DS), is served by wave w for every product (by two waves in the
+// 8-wave variants below). Per key tile t there are three stages:
 //
 //   A(t) similarity S^T = Z_keys . Q^T over the wave's slice (v_mfma_f32_16x16x32):
 //        an fp32 partial per wave of exact 16-bit products. The same registers
@@ -24,14 +24,22 @@
 //
 // so the reduction's VALU work overlaps the similarity MFMAs. A(t) keeps its
 // partial S^T in registers until interval 2, which lets one LDS buffer hold the
-// partials; the staged key rows are double-buffered (C(t-1) reads one buffer
-// while A(t) fills the other).
+// partials; the key tiles sit in a ring of 2 or 3 LDS slots, refilled by
+// buffer-to-LDS copies a tile or two ahead.
 //
-// The 16-row variants run 8 waves instead: waves 0-3 do A, C and the staging as
-// above, waves 4-7 ("helpers", one per feature slice) do B, the V loads, the key
-// norm reciprocals and the key-tile refills, in a program of their own that passes
-// the same barriers. Each SIMD then holds a product wave and a helper wave, and
-// the reduction and the memory traffic no longer stall the MFMAs.
+// Waves per workgroup (fused_threads in avey_common.h):
+//   * 16-row variants, 8 waves ("warp specialization"): waves 0-3 do A, C and T,
+//     waves 4-7 ("helpers", one per feature slice) do B, the V loads, the key norm
+//     reciprocals and the key-tile copies, in a program of their own that passes the
+//     same barriers. Each SIMD holds a product wave and a helper wave, and the
+//     reduction and the memory traffic no longer stall the MFMAs.
+//   * 32-row variants and 64-row ones up to 128 features per slice, 8 waves ("query
+//     split"): waves w and w+4 serve slice w, each for half of the query blocks, so
+//     each holds half the accumulators. Each copies half of a key tile's rows and
+//     orders them for its partner by an explicit wait before the iteration's last
+//     barrier.
+//   * 64-row variants with 192 features per slice, 4 waves of 512 registers (their
+//     state does not fit 256).
 //
 // The epilogue multiplies by 1 / (den + eps), adds bias, applies the activation,
 // multiplies by the gate, zeroes padded rows and rounds once (ops.py:79-91).
