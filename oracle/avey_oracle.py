@@ -29,6 +29,9 @@ Pinning (each check lives in ``tests/test_oracle.py``):
   random inputs with every flag combination; invariants (causal output rows
   depend only on earlier rows; permuting keys in the bidirectional case
   leaves outputs unchanged; NaN in masked rows never reaches valid outputs).
+* ``contextualize_backward``: central finite differences of ``contextualize``
+  in fp64 on small inputs, and PyTorch autograd over the product's eager path
+  (a restatement of ``_reference`` that autograd differentiates on its own).
 * ``key_tile_count``: the reference's closed-form table
   (``tests/test_causal_skip.py:52-60``) and a brute-force count of tiles
   holding at least one allowed (query, key) pair.
@@ -167,3 +170,97 @@ def row_condition(z_tr, valid=None, *, eps=1e-6, norm_eps=1e-12):
     if valid is not None:
         s = np.where(valid[:, None, :], s, 0.0)
     return np.sum(np.abs(s), -1) / np.abs(np.sum(s, -1) + eps)
+
+
+def activate_grad(x, activation):
+    """d act(x) / dx for the activations of ``avey_kernels/ops.py:49-58``.
+
+    The reference has no written backward: its gradients are PyTorch autograd
+    over ``_reference`` (``ops.py:96-106``), so these are the derivatives
+    autograd takes. relu: 1 where x > 0 (threshold_backward); relu2: 2 max(x, 0);
+    silu: s (1 + x (1 - s)) with s = sigmoid(x); gelu (tanh form):
+    0.5 (1 + t) + 0.5 x (1 - t^2) k (1 + 3 * 0.044715 x^2), t = tanh(k (x + 0.044715 x^3)).
+    """
+    one = x.dtype.type(1)
+    if activation == 'identity':
+        return np.ones_like(x)
+    if activation == 'relu':
+        return (x > 0).astype(x.dtype)
+    if activation == 'relu2':
+        return 2 * np.maximum(x, 0)
+    if activation == 'silu':
+        s = _sigmoid(x)
+        return s * (one + x * (one - s))
+    if activation == 'gelu':
+        t = np.tanh(_GELU_K * (x + 0.044715 * x * x * x))
+        return 0.5 * (one + t) + 0.5 * x * (one - t * t) * _GELU_K * (one + 3 * 0.044715 * x * x)
+    raise ValueError(f'unknown activation {activation!r}')
+
+
+def contextualize_backward(dout, z_tr, v=None, z_tl=None, bias=None, valid=None, *, eps, norm_eps,
+                           causal, normalize, activation, acc=np.float64, _plant=None):
+    """Gradients of ``contextualize`` (the ``_reference`` math, ``ops.py:61-91``).
+
+    Returns ``(dz_tr, dv, dz_tl, dbias)``, unrounded in ``acc``; entries for
+    absent inputs are None. Written as the closed-form chain rule (no autograd),
+    per batch item with P = S * V * M, y = num / den (normalize) or num,
+    u = y + bias, r the valid-row mask:
+
+    * dz_tl = dout * act(u) * r;  du = dout * gate * act'(u) * r;  dbias = sum du
+    * normalize: dnum = du / den, dden_i = -sum_d du_id y_id / den_i; else dnum = du, dden = 0
+    * dP_ij = dnum_i . z_j + dden_i;  dS = dP * V * M;  dv = sum_b dP * S * M
+    * dz = r * (P^T dnum + J(dzhat)),  dzhat = dS zhat + dS^T zhat,
+      J(x) = (x - zhat (zhat . x)) / ||z|| where ||z|| >= norm_eps, else x / norm_eps
+      (F.normalize divides by clamp_min(||z||, norm_eps); the clamp passes no
+      gradient to the norm below it).
+
+    ``_plant`` injects a named mistake ('no_radial', 'no_transpose',
+    'dden_sign') so the tests can show their checks catch it.
+    """
+    z = np.array(z_tr, dtype=acc, copy=True)
+    g = np.array(dout, dtype=acc, copy=True)
+    bsz, c, d = z.shape
+    r = np.ones((bsz, c), dtype=bool) if valid is None else np.asarray(valid, dtype=bool)
+    z = np.where(r[:, :, None], z, acc(0))
+    g = np.where(r[:, :, None], g, acc(0))
+    norms = np.sqrt(np.sum(z * z, axis=-1, keepdims=True))
+    denom = np.maximum(norms, acc(norm_eps))
+    zn = z / denom
+    s = np.matmul(zn, np.swapaxes(zn, 1, 2))
+    mask = np.broadcast_to(r[:, None, :], s.shape).copy()
+    if causal:
+        mask &= np.tril(np.ones((c, c), dtype=bool))[None]
+    w = mask.astype(acc)
+    if v is not None:
+        w = w * np.asarray(v, dtype=acc)[None]
+    p = s * w
+    num = np.matmul(p, z)
+    den = np.sum(p, axis=-1, keepdims=True) + acc(eps) if normalize else None
+    y = num / den if normalize else num
+    u = y + (np.asarray(bias, dtype=acc) if bias is not None else acc(0))
+    a = activate(u, activation)
+    if z_tl is not None:
+        gate = np.where(r[:, :, None], np.asarray(z_tl, dtype=acc), acc(0))
+        dz_tl = g * a
+        du = g * gate * activate_grad(u, activation)
+    else:
+        dz_tl = None
+        du = g * activate_grad(u, activation)
+    dbias = du.sum(axis=(0, 1)) if bias is not None else None
+    if normalize:
+        dnum = du / den
+        dden = -np.sum(du * y, axis=-1, keepdims=True) / den
+        if _plant == 'dden_sign':
+            dden = -dden
+    else:
+        dnum = du
+        dden = np.zeros((bsz, c, 1), dtype=acc)
+    dp = np.matmul(dnum, np.swapaxes(z, 1, 2)) + dden
+    ds = dp * w
+    dv = np.sum(dp * s * mask, axis=0) if v is not None else None
+    dzn = np.matmul(ds, zn) + (0 if _plant == 'no_transpose' else np.matmul(np.swapaxes(ds, 1, 2), zn))
+    radial = 0 if _plant == 'no_radial' else np.sum(zn * dzn, axis=-1, keepdims=True)
+    dz_norm = np.where(norms >= acc(norm_eps), (dzn - zn * radial) / denom, dzn / acc(norm_eps))
+    dz = np.matmul(np.swapaxes(p, 1, 2), dnum) + dz_norm
+    dz = np.where(r[:, :, None], dz, acc(0))
+    return dz, dv, dz_tl, dbias
