@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG_DIR, 'csrc')
 INCLUDE = os.path.join(REPO_DIR, 'include')
 BUILD_DIR = os.path.join(PKG_DIR, '_build')
 LIB_PATH = os.path.join(PKG_DIR, 'libavey_hip.so')
-SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip') + tuple(
+SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip', 'avey_backward.hip') + tuple(
     f'avey_fused_bm{bm}_{t}{k}.hip' for k in ('', '_strided') for bm in (64, 32, 16) for t in ('bf16', 'f16'))
 ARCH = 'gfx950'
 

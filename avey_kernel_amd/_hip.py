@@ -9,6 +9,10 @@ and z_tl may be strided views whose last dimension is contiguous (e.g. the two
 halves of the enricher output): their row and batch strides go to the library
 instead of a copy (the reference copies them, ``avey_kernels/ops.py:109-113``).
 
+Its gradient is ``avey_kernels::contextualize_backward``, the library's fused
+backward (the reference differentiates its eager path with autograd instead,
+``avey_kernels/ops.py:96-106``).
+
 Nothing here falls back to another implementation: if the shared library is
 missing or refuses the call, the error surfaces to the caller.
 """
@@ -42,6 +46,13 @@ class AveyFwdArgs(ctypes.Structure):
     ]
 
 
+class AveyBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ('fwd', AveyFwdArgs), ('dout', ctypes.c_void_p), ('dz_tr', ctypes.c_void_p), ('dv', ctypes.c_void_p),
+        ('dz_tl', ctypes.c_void_p), ('dbias', ctypes.c_void_p),
+    ]
+
+
 class AveyFwdPlan(ctypes.Structure):
     _fields_ = [
         ('kernel', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
@@ -57,12 +68,14 @@ EXPORTS = {
     'avey_fwd_plan': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.POINTER(AveyFwdPlan)]),
     'avey_key_tile_count': (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                              ctypes.c_int32, ctypes.c_int32]),
+    'avey_bwd': (ctypes.c_int, [ctypes.POINTER(AveyBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    'avey_bwd_workspace_bytes': (ctypes.c_int64, [ctypes.POINTER(AveyBwdArgs)]),
     'avey_device_supported': (ctypes.c_int, [ctypes.c_int]),
     'avey_status_string': (ctypes.c_char_p, [ctypes.c_int]),
     'avey_abi_version': (ctypes.c_int, []),
     'avey_debug_poison_lds': (ctypes.c_int, [ctypes.c_void_p]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 
@@ -189,3 +202,90 @@ def contextualize(z_tr: torch.Tensor, v: Optional[torch.Tensor], z_tl: Optional[
 @contextualize.register_fake
 def _contextualize_fake(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation):
     return torch.empty_like(z_tr, memory_format=torch.contiguous_format)
+
+
+# Limits of the fused backward (avey_bwd); other inputs take autograd over the eager path.
+BWD_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+BWD_MAX_FEATURES = 1024
+BWD_MAX_BATCH = 65535
+
+
+def backward_supported(z_tr):
+    """True when avey_bwd covers gradients of a call on ``z_tr`` (dtype and shape only)."""
+    return (z_tr.dtype in BWD_DTYPES and z_tr.shape[2] <= BWD_MAX_FEATURES
+            and z_tr.shape[0] <= BWD_MAX_BATCH)
+
+
+def launch_backward(dout, z_tr, v, z_tl, bias, valid, dz_tr, dv, dz_tl, dbias, eps, norm_eps, causal,
+                    normalize, activation):
+    """Launch the backward into the given gradient buffers (None: not computed) on
+    the current stream of z_tr's device. Every [B, C, D] operand is contiguous."""
+    lib = load()
+    valid_u8 = valid.view(torch.uint8) if valid is not None else None
+    fwd = make_args(z_tr, v, z_tl, bias, valid_u8, None, eps, norm_eps, causal, normalize, activation)
+    args = AveyBwdArgs(fwd, _ptr(dout), _ptr(dz_tr), _ptr(dv), _ptr(dz_tl), _ptr(dbias))
+    need = lib.avey_bwd_workspace_bytes(ctypes.byref(args))
+    if need < 0:
+        raise ValueError(f'avey_bwd: {status_string(int(need))}')
+    work = torch.empty(int(need), dtype=torch.uint8, device=z_tr.device)
+    with torch.cuda.device(z_tr.device):
+        stream = torch.cuda.current_stream(z_tr.device).cuda_stream
+        st = lib.avey_bwd(ctypes.byref(args), _ptr(work), int(need), stream)
+    if st < 0:
+        raise ValueError(f'avey_bwd: {status_string(st)}')
+    if st > 0:
+        raise RuntimeError(f'avey_bwd: HIP error {st}: {status_string(st)}')
+
+
+def _nothing(t):
+    return t.new_empty((0,))
+
+
+@torch.library.custom_op('avey_kernels::contextualize_backward', mutates_args=())
+def contextualize_backward(dout: torch.Tensor, z_tr: torch.Tensor, v: Optional[torch.Tensor],
+                           z_tl: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+                           valid: Optional[torch.Tensor], eps: float, norm_eps: float, causal: bool,
+                           normalize: bool, activation: str, need_v: bool, need_z_tl: bool,
+                           need_bias: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dz_tr, dv, dz_tl, dbias) of ``contextualize``; a gradient that is not
+    needed (or whose input is absent) comes back as an empty tensor."""
+    z_tr, dout = z_tr.contiguous(), dout.contiguous()
+    z_tl = z_tl.contiguous() if z_tl is not None else None
+    v, bias, valid = (None if t is None else t.contiguous() for t in (v, bias, valid))
+    dz_tr = torch.empty_like(z_tr)
+    dv = torch.empty_like(v) if (v is not None and need_v) else None
+    dz_tl = torch.empty_like(z_tl) if (z_tl is not None and need_z_tl) else None
+    dbias = torch.empty_like(bias) if (bias is not None and need_bias) else None
+    launch_backward(dout, z_tr, v, z_tl, bias, valid, dz_tr, dv, dz_tl, dbias, eps, norm_eps, causal,
+                    normalize, activation)
+    return (dz_tr, _nothing(z_tr) if dv is None else dv, _nothing(z_tr) if dz_tl is None else dz_tl,
+            _nothing(z_tr) if dbias is None else dbias)
+
+
+@contextualize_backward.register_fake
+def _contextualize_backward_fake(dout, z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation,
+                                 need_v, need_z_tl, need_bias):
+    def grad_like(t, need):
+        return torch.empty_like(t, memory_format=torch.contiguous_format) if (t is not None and need) \
+            else z_tr.new_empty((0,))
+    return (torch.empty_like(z_tr, memory_format=torch.contiguous_format), grad_like(v, need_v),
+            grad_like(z_tl, need_z_tl), grad_like(bias, need_bias))
+
+
+def _setup_context(ctx, inputs, output):
+    z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation = inputs
+    ctx.save_for_backward(z_tr, v, z_tl, bias, valid)
+    ctx.flags = (eps, norm_eps, causal, normalize, activation)
+
+
+def _backward(ctx, grad):
+    z_tr, v, z_tl, bias, valid = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    dz_tr, dv, dz_tl, dbias = torch.ops.avey_kernels.contextualize_backward(
+        grad, z_tr, v, z_tl, bias, valid, *ctx.flags, bool(need[1]), bool(need[2]), bool(need[3]))
+    return (dz_tr if need[0] else None, dv if (v is not None and need[1]) else None,
+            dz_tl if (z_tl is not None and need[2]) else None,
+            dbias if (bias is not None and need[3]) else None, None, None, None, None, None, None)
+
+
+contextualize.register_autograd(_backward, setup_context=_setup_context)

@@ -1,0 +1,545 @@
+// Backward of the contextualizer on gfx950: gradients w.r.t. z_tr, v, z_tl and
+// bias, computed without storing any C x C tile in HBM.
+//
+// The reference has no written backward: gradients are autograd over its eager
+// path (avey_kernels/ops.py:96-106, :61-91), which materialises [B, C, C]. Here,
+// per batch item, with P = S * V * M (S the cosine similarity, M the causal /
+// key-padding mask), y = num / den (normalize) or num, u = y + bias, r the
+// valid-row mask and g the incoming gradient:
+//   dz_tl = g * act(u) * r,  du = g * gate * act'(u) * r,  dbias = sum du,
+//   dnum = du / den, dden_i = -sum_d du_id y_id / den_i   (normalize; else du, 0),
+//   dP_ij = dnum_i . z_j + dden_i,  dS = dP * V * M,  dv = sum_b dP * S * M,
+//   dz = r * (P^T dnum + J(dS zhat + dS^T zhat)),
+//   J(x) = (x - zhat (zhat . x)) / ||z||  (||z|| >= norm_eps), else x / norm_eps.
+//
+// Kernels (all fp32 arithmetic, fp32 MFMA v_mfma_f32_16x16x4f32):
+//   bwd_prep   row norms ||z|| of the masked rows; clears the dv / dbias accumulators.
+//   bwd_rows   one workgroup per (batch item, 16 query rows). Pass 1 over key
+//              tiles recomputes S, P, num and den (the forward); the epilogue
+//              writes dz_tl, dnum, dden and adds dbias. Pass 2 recomputes S, forms
+//              dP = dnum z^T + dden and dS, adds dP * S into dv and accumulates the
+//              query-side dS zhat, written to the workspace.
+//   bwd_cols   one workgroup per (batch item, 16 key rows), over query tiles:
+//              P^T dnum and the key-side dS^T zhat, then J and the row mask; writes
+//              dz_tr.
+//   bwd_final  dv and dbias cast from their fp32 accumulators.
+// A workgroup is 4 waves. Products that contract over features ("row dots":
+// S, dP) give each wave 16 of the 64 keys (or queries) of a tile; products that
+// contract over rows (P z, dS z, P^T dnum, dS^T z) give each wave every fourth
+// 16-column tile of the [16, D] accumulator, with the [16, 64] P / dS tile passed
+// through LDS. Operand rows are read from global memory (they stay in L1 / L2);
+// rows of padded tokens are never loaded, so NaN padding reaches nothing.
+#include <math.h>
+
+#include "avey_common.h"
+#include "avey_internal.h"
+
+namespace avey {
+
+namespace {
+
+constexpr int kRows = 16;      // query (bwd_rows) or key (bwd_cols) rows per workgroup
+constexpr int kTile = 64;      // rows of the other side per pipeline step
+constexpr int kPitch = kTile + 4;  // LDS row pitch of a [16][64] tile (floats)
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Element loads converted to fp32.
+template <typename T> struct Io;
+template <> struct Io<float> {
+  __device__ static float one(const float* p) { return *p; }
+  __device__ static f32x4 four(const float* p) { return *(const f32x4*)p; }
+  __device__ static void put(float* p, float x) { *p = x; }
+};
+template <> struct Io<__bf16> {
+  __device__ static float one(const __bf16* p) { return (float)*p; }
+  __device__ static f32x4 four(const __bf16* p) {
+    u32x2 u = *(const u32x2*)p;
+    return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                 __uint_as_float(u.y & 0xffff0000u)};
+  }
+  __device__ static void put(__bf16* p, float x) { *p = (__bf16)x; }
+};
+template <> struct Io<_Float16> {
+  __device__ static float one(const _Float16* p) { return (float)*p; }
+  __device__ static f32x4 four(const _Float16* p) {
+    f16x4 h = *(const f16x4*)p;
+    return f32x4{(float)h.x, (float)h.y, (float)h.z, (float)h.w};
+  }
+  __device__ static void put(_Float16* p, float x) { *p = (_Float16)x; }
+};
+
+// Four consecutive features d..d+3 of one row (zero past D). `vec`: rows are
+// 4-element aligned (D % 4 == 0), so a vector load is in bounds when d + 4 <= D.
+template <typename T>
+__device__ __forceinline__ f32x4 row4(const T* row, int d, int D, bool vec) {
+  if (vec && d + 4 <= D) return Io<T>::four(row + d);
+  f32x4 x = {0.f, 0.f, 0.f, 0.f};
+  if (d < D) x[0] = Io<T>::one(row + d);
+  if (d + 1 < D) x[1] = Io<T>::one(row + d + 1);
+  if (d + 2 < D) x[2] = Io<T>::one(row + d + 2);
+  if (d + 3 < D) x[3] = Io<T>::one(row + d + 3);
+  return x;
+}
+
+// 16 x 16 block of A B^T contracted over D features. A row lr of the block is
+// `a` (scaled by sa), B row lr is `b` (scaled by sb); a null row contributes
+// zeros and is not read. Lane (lg, lr) feeds features 16s + 4lg + t at sub-step
+// t of step s to both operands (any bijection of the contracted index gives the
+// same sum), so every load is four consecutive features. Result: lane holds
+// C[4 lg + i][lr], i = 0..3.
+template <typename TA, typename TB>
+__device__ __forceinline__ f32x4 row_dot(const TA* a, float sa, const TB* b, float sb, int D, bool vec, int lg) {
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  const int steps = (D + 15) >> 4;
+  for (int s = 0; s < steps; ++s) {
+    const int d = 16 * s + 4 * lg;
+    f32x4 x = a ? row4<TA>(a, d, D, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 y = b ? row4<TB>(b, d, D, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) c = mfma4(x[t] * sa, y[t] * sb, c);
+  }
+  return c;
+}
+
+// acc[t] (16 x 16, columns 16 (w + 4t) ..) += A (16 x 64, LDS, pitch kPitch)
+// times rows r0 .. r0+63 of Y (row stride D). Row r0 + 4s + lg is read only when
+// bit s of `rows_ok` is set.
+template <typename T, int MAXT>
+__device__ __forceinline__ void rows_acc(f32x4 (&acc)[MAXT], const float* A, const T* Y, int64_t r0, uint32_t rows_ok,
+                                         int D, int w, int lr, int lg) {
+  float af[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) af[s] = A[lr * kPitch + 4 * s + lg];
+  const int ntiles = (D + 15) >> 4;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile = w + 4 * t;
+    if (tile >= ntiles) break;
+    const int col = 16 * tile + lr;
+    const T* y = Y + (r0 + lg) * (int64_t)D + col;
+    float yv[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      yv[s] = (((rows_ok >> s) & 1u) && col < D) ? Io<T>::one(y + (int64_t)(4 * s) * D) : 0.f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) acc[t] = mfma4(af[s], yv[s], acc[t]);
+  }
+}
+
+__device__ __forceinline__ bool row_valid(const uint8_t* valid, int64_t b, int64_t C, int64_t row) {
+  return row < C && (!valid || valid[b * C + row] != 0);
+}
+
+__device__ __forceinline__ float inv_norm(const float* nrm, int64_t idx, float norm_eps) {
+  return 1.f / fmaxf(nrm[idx], norm_eps);
+}
+
+// Sum over the 16 lanes of a lane group (lanes sharing lg).
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+
+// d act(u) / du; the derivatives autograd takes of ops.py:49-58.
+__device__ __forceinline__ float act_grad(float x, int act) {
+  switch (act) {
+    case AVEY_ACT_RELU: return x > 0.f ? 1.f : 0.f;
+    case AVEY_ACT_RELU2: return x > 0.f ? 2.f * x : 0.f;
+    case AVEY_ACT_SILU: {
+      float e = expf(-fabsf(x));
+      float s = x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+      return s * (1.f + x * (1.f - s));
+    }
+    case AVEY_ACT_GELU: {
+      const float k = 0.7978845608028654f;
+      float t = tanhf(k * (x + 0.044715f * x * x * x));
+      return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * k * (1.f + 3.f * 0.044715f * x * x);
+    }
+    default: return 1.f;
+  }
+}
+
+struct Ws {
+  float *nrm, *dnum, *dden, *dzr, *dv, *db;
+};
+
+// Workspace layout (fp32, each part 256-byte aligned): nrm [B*C], dden [B*C],
+// dnum [B*C*D], dzr [B*C*D], then dv [C*C] and dbias [D] when present.
+__host__ __device__ inline int64_t up64(int64_t n) { return (n + 63) & ~int64_t(63); }
+
+__host__ inline Ws carve(void* base, int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
+  float* p = (float*)base;
+  Ws w;
+  w.nrm = p; p += up64(B * C);
+  w.dden = p; p += up64(B * C);
+  w.dnum = p; p += up64(B * C * D);
+  w.dzr = p; p += up64(B * C * D);
+  w.dv = has_v ? p : nullptr; p += has_v ? up64(C * C) : 0;
+  w.db = has_bias ? p : nullptr;
+  return w;
+}
+
+__host__ inline int64_t ws_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
+  return 2 * up64(B * C) + 2 * up64(B * C * D) + (has_v ? up64(C * C) : 0) + (has_bias ? up64(D) : 0);
+}
+
+// One wave per row: ||z|| of the masked row. Every thread also clears a share of
+// the dv / dbias accumulators.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p, Ws ws) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t rows = p.B * p.C;
+  if (row < rows) {
+    const int64_t b = row / p.C, c = row % p.C;
+    float ss = 0.f;
+    if (row_valid(p.valid, b, p.C, c)) {
+      const T* z = (const T*)p.z + row * p.D;
+      for (int64_t d = lane; d < p.D; d += 64) {
+        float x = Io<T>::one(z + d);
+        ss += x * x;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) ws.nrm[row] = sqrtf(ss);
+  }
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (int64_t)gridDim.x * blockDim.x;
+  if (ws.dv)
+    for (int64_t i = tid; i < p.C * p.C; i += nt) ws.dv[i] = 0.f;
+  if (ws.db)
+    for (int64_t i = tid; i < p.D; i += nt) ws.db[i] = 0.f;
+}
+
+template <typename T, int MAXT>
+__global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
+  constexpr int dp = 64 * MAXT + 4;          // pitch of dnl; D <= 64 * MAXT
+  __shared__ float tile[kRows * kPitch];     // [16][kPitch]: P, then dS * inv(key)
+  __shared__ float red[4 * kRows];           // [4 waves][16]
+  __shared__ float stat[2 * kRows];          // den, dden of the block's rows
+  __shared__ __attribute__((aligned(16))) float dnl[kRows * dp];  // dnum of the block's rows
+  const int D = (int)p.D;
+  const int64_t C = p.C, b = blockIdx.y, q0 = (int64_t)blockIdx.x * kRows;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const bool vec = (D & 3) == 0;
+  const float neps = (float)p.norm_eps;
+  const T* zb = (const T*)p.z + b * C * D;
+  const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
+  const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
+  const T* vt = (const T*)p.v;
+
+  // A-operand rows of the row dots: query q0 + lr.
+  const int64_t qa = q0 + lr;
+  const bool qa_ok = row_valid(p.valid, b, C, qa);
+  const T* qa_row = qa_ok ? zb + qa * D : nullptr;
+  const float qa_inv = qa_ok ? inv_norm(ws.nrm, b * C + qa, neps) : 0.f;
+
+  // ---- pass 1: num, den ----
+  f32x4 acc[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float den4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k = kt * kTile + 16 * w + lr;  // this lane's key (B row, output column)
+    const bool k_ok = row_valid(p.valid, b, C, k);
+    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    f32x4 s4 = row_dot<T, T>(qa_row, qa_inv, k_ok ? zb + k * D : nullptr, k_inv, D, vec, lg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      float pv = 0.f;
+      if (m) pv = s4[i] * (vt ? Io<T>::one(vt + q * C + k) : 1.f);
+      den4[i] += pv;
+      tile[(4 * lg + i) * kPitch + 16 * w + lr] = pv;
+    }
+    uint32_t rows_ok = 0;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) rows_ok |= (uint32_t)row_valid(p.valid, b, C, kt * kTile + 4 * s + lg) << s;
+    __syncthreads();
+    rows_acc<T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(den4[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    stat[i] = red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i] + (float)p.eps;
+  }
+  __syncthreads();
+
+  // ---- epilogue 1: dz_tl, dnum, dden, dbias ----
+  const int ntiles = (D + 15) >> 4;
+  float ddp[4] = {0.f, 0.f, 0.f, 0.f};
+  const T* gb = p.gate ? (const T*)p.gate + b * C * D : nullptr;
+  const T* ob = (const T*)p.dout + b * C * D;
+  T* dgb = p.dgate ? (T*)p.dgate + b * C * D : nullptr;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+    float dbs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * lg + i;
+      const int64_t q = q0 + row;
+      float dn = 0.f;
+      if (col < D && q < C) {
+        const bool rq = row_valid(p.valid, b, C, q);
+        const float den = stat[row];
+        const float y = p.normalize ? acc[t][i] / den : acc[t][i];
+        const float u = y + (p.bias ? Io<T>::one((const T*)p.bias + col) : 0.f);
+        const float go = rq ? Io<T>::one(ob + q * D + col) : 0.f;
+        const float gt = gb ? (rq ? Io<T>::one(gb + q * D + col) : 0.f) : 1.f;
+        if (dgb) Io<T>::put(dgb + q * D + col, go * activate<float>(u, p.act));
+        const float du = go * gt * act_grad(u, p.act);
+        dbs += du;
+        dn = p.normalize ? du / den : du;
+        ddp[i] += du * y;
+        ws.dnum[(b * C + q) * D + col] = dn;
+      }
+      dnl[row * dp + col] = dn;
+    }
+    if (ws.db) {
+      dbs += __shfl_xor(dbs, 16);
+      dbs += __shfl_xor(dbs, 32);
+      if (lg == 0 && col < D) unsafeAtomicAdd(ws.db + col, dbs);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(ddp[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    const int64_t q = q0 + i;
+    float dd = 0.f;
+    if (p.normalize) dd = -(red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / stat[i];
+    stat[kRows + i] = dd;
+    if (q < C) ws.dden[b * C + q] = dd;
+  }
+  __syncthreads();
+
+  // ---- pass 2: dP, dS, dv, dS zhat ----
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* dn_row = dnl + lr * dp;  // A rows of dP = dnum z^T (zeros for rows past C)
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k = kt * kTile + 16 * w + lr;
+    const bool k_ok = row_valid(p.valid, b, C, k);
+    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    const T* k_row = k_ok ? zb + k * D : nullptr;
+    f32x4 s4 = row_dot<T, T>(qa_row, qa_inv, k_row, k_inv, D, vec, lg);
+    f32x4 d4 = row_dot<float, T>(dn_row, 1.f, k_row, 1.f, D, vec, lg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      float dsv = 0.f;
+      if (m) {
+        const float dpv = d4[i] + stat[kRows + 4 * lg + i];
+        const float vv = vt ? Io<T>::one(vt + q * C + k) : 1.f;
+        dsv = dpv * vv * k_inv;
+        if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i]);
+      }
+      tile[(4 * lg + i) * kPitch + 16 * w + lr] = dsv;
+    }
+    uint32_t rows_ok = 0;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) rows_ok |= (uint32_t)row_valid(p.valid, b, C, kt * kTile + 4 * s + lg) << s;
+    __syncthreads();
+    rows_acc<T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      if (col < D && q < C) ws.dzr[(b * C + q) * D + col] = acc[t][i];
+    }
+  }
+}
+
+template <typename T, int MAXT>
+__global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
+  __shared__ float pt[kRows * kPitch];  // P^T tile [16 keys][64 queries]
+  __shared__ float dt[kRows * kPitch];  // (dS * inv(query))^T tile
+  __shared__ float red[4 * kRows];
+  __shared__ float rad[kRows];
+  const int D = (int)p.D;
+  const int64_t C = p.C, b = blockIdx.y, k0 = (int64_t)blockIdx.x * kRows;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const bool vec = (D & 3) == 0;
+  const float neps = (float)p.norm_eps;
+  const T* zb = (const T*)p.z + b * C * D;
+  const float* dnb = ws.dnum + b * C * D;
+  const T* vt = (const T*)p.v;
+
+  const int64_t ka = k0 + lr;  // A row of the row dots: key k0 + lr
+  const bool ka_ok = row_valid(p.valid, b, C, ka);
+  const T* ka_row = ka_ok ? zb + ka * D : nullptr;
+  const float ka_inv = ka_ok ? inv_norm(ws.nrm, b * C + ka, neps) : 0.f;
+
+  f32x4 acc1[MAXT], acc2[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t qstart = p.causal ? k0 : 0;
+  for (int64_t qt = qstart; qt < C; qt += kTile) {
+    const int64_t q = qt + 16 * w + lr;  // this lane's query (B row, output column)
+    const bool q_in = q < C;
+    const bool q_ok = row_valid(p.valid, b, C, q);
+    const float q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
+    f32x4 s4 = row_dot<T, T>(ka_row, ka_inv, q_ok ? zb + q * D : nullptr, q_inv, D, vec, lg);
+    f32x4 d4 = row_dot<T, float>(ka_row, 1.f, q_in ? dnb + q * D : nullptr, 1.f, D, vec, lg);
+    const float dd = q_in ? ws.dden[b * C + q] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      const bool m = q_in && row_valid(p.valid, b, C, k) && (!p.causal || k <= q);
+      float pv = 0.f, dsv = 0.f;
+      if (m) {
+        const float vv = vt ? Io<T>::one(vt + q * C + k) : 1.f;
+        pv = s4[i] * vv;
+        dsv = (d4[i] + dd) * vv * q_inv;
+      }
+      pt[(4 * lg + i) * kPitch + 16 * w + lr] = pv;
+      dt[(4 * lg + i) * kPitch + 16 * w + lr] = dsv;
+    }
+    uint32_t in_ok = 0, rows_ok = 0;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int64_t r = qt + 4 * s + lg;
+      in_ok |= (uint32_t)(r < C) << s;
+      rows_ok |= (uint32_t)row_valid(p.valid, b, C, r) << s;
+    }
+    __syncthreads();
+    rows_acc<float, MAXT>(acc1, pt, dnb, qt, in_ok, D, w, lr, lg);
+    rows_acc<T, MAXT>(acc2, dt, zb, qt, rows_ok, D, w, lr, lg);
+    __syncthreads();
+  }
+
+  // Epilogue: dzhat = key-side + query-side parts; J; row mask.
+  const int ntiles = (D + 15) >> 4;
+  float rp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      if (col < D && row_valid(p.valid, b, C, k)) {
+        const float g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
+        acc2[t][i] = g;
+        rp[i] += Io<T>::one(zb + k * D + col) * g;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(rp[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    const int64_t k = k0 + i;
+    float r = 0.f;
+    if (row_valid(p.valid, b, C, k)) {
+      const float n = ws.nrm[b * C + k];
+      // zhat . dzhat / ||z|| when the norm is not clamped; no radial term otherwise.
+      if (n >= neps) r = (red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / n;
+    }
+    rad[i] = r;
+  }
+  __syncthreads();
+  T* dzb = (T*)p.dz + b * C * D;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      if (col >= D || k >= C) continue;
+      float g = 0.f;
+      if (row_valid(p.valid, b, C, k)) {
+        const float inv = inv_norm(ws.nrm, b * C + k, neps);
+        const float zh = Io<T>::one(zb + k * D + col) * inv;
+        g = acc1[t][i] + (acc2[t][i] - zh * rad[4 * lg + i]) * inv;
+      }
+      Io<T>::put(dzb + k * D + col, g);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, Ws ws) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (int64_t)gridDim.x * blockDim.x;
+  if (p.dv)
+    for (int64_t i = tid; i < p.C * p.C; i += nt) Io<T>::put((T*)p.dv + i, ws.dv[i]);
+  if (p.dbias)
+    for (int64_t i = tid; i < p.D; i += nt) Io<T>::put((T*)p.dbias + i, ws.db[i]);
+}
+
+template <typename T, int MAXT>
+hipError_t launch_bwd_t(const BwdParams& p, hipStream_t s) {
+  Ws ws = carve(p.work, p.B, p.C, p.D, p.v != nullptr, p.bias != nullptr);
+  const int64_t rows = p.B * p.C;
+  hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
+  const dim3 grid((unsigned)cdiv(p.C, kRows), (unsigned)p.B);
+  hipLaunchKernelGGL((bwd_rows_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd_cols_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
+  if (p.dv || p.dbias) {
+    const int64_t n = p.dv ? p.C * p.C : p.D;
+    const int64_t blocks = cdiv(n, 256) < 1024 ? cdiv(n, 256) : 1024;
+    hipLaunchKernelGGL(bwd_final_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_bwd_d(const BwdParams& p, hipStream_t s) {
+  const int64_t tiles = cdiv(p.D, 16);
+  if (tiles <= 8) return launch_bwd_t<T, 2>(p, s);
+  if (tiles <= 16) return launch_bwd_t<T, 4>(p, s);
+  if (tiles <= 32) return launch_bwd_t<T, 8>(p, s);
+  return launch_bwd_t<T, 16>(p, s);
+}
+
+}  // namespace
+
+int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
+  return ws_floats(B, C, D, has_v, has_bias);
+}
+
+hipError_t launch_bwd(const BwdParams& p, int dtype, hipStream_t s) {
+  switch (dtype) {
+    case AVEY_DTYPE_BF16: return launch_bwd_d<__bf16>(p, s);
+    case AVEY_DTYPE_F16: return launch_bwd_d<_Float16>(p, s);
+    case AVEY_DTYPE_F32: return launch_bwd_d<float>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace avey

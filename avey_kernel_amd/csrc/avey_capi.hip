@@ -193,6 +193,8 @@ const char* avey_status_string(int status) {
     case AVEY_ERR_FLAGS: return "causal and normalize must be 0 or 1";
     case AVEY_ERR_ALIAS: return "out overlaps an input buffer";
     case AVEY_ERR_STRIDE: return "z_tr / z_tl row stride below features, or a negative stride";
+    case AVEY_ERR_UNSUPPORTED:
+      return "backward needs bf16 / fp16 / fp32, features <= 1024, batch <= 65535 and contiguous operands";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
   }
 }
@@ -227,6 +229,79 @@ int avey_fwd_plan(const avey_fwd_args* args, avey_fwd_plan_t* out) {
 }
 
 int avey_device_supported(int device) { return device_ok(device) ? 1 : 0; }
+
+namespace {
+// Checks of avey_bwd's arguments; on success fills the kernel parameters.
+int validate_bwd(const avey_bwd_args* a, BwdParams* p) {
+  if (!a || !a->dout || !a->dz_tr) return AVEY_ERR_NULL_POINTER;
+  avey_fwd_args f = a->fwd;
+  f.out = a->dz_tr;  // the forward's checks, with dz_tr as the output that must not alias an input
+  int st = validate(&f);
+  if (st != AVEY_OK) return st;
+  if (f.dtype == AVEY_DTYPE_F64 || f.features > kBwdMaxFeatures || f.batch > 65535 || f.z_tr_row_stride != 0 ||
+      f.z_tl_row_stride != 0)
+    return AVEY_ERR_UNSUPPORTED;
+  const size_t es = elem_size(f.dtype);
+  const size_t nb = (size_t)f.batch * (size_t)f.context * (size_t)f.features * es;
+  const size_t vb = (size_t)f.context * (size_t)f.context * es;
+  void* dv = f.v ? a->dv : nullptr;
+  void* dg = f.z_tl ? a->dz_tl : nullptr;
+  void* db = f.bias ? a->dbias : nullptr;
+  const struct { const void* p; size_t n; } outs[] = {{a->dz_tr, nb}, {dv, vb}, {dg, nb}, {db, f.features * es}};
+  const struct { const void* p; size_t n; } ins[] = {{f.z_tr, nb}, {f.v, vb}, {f.z_tl, nb}, {f.bias, f.features * es},
+                                                     {f.valid, (size_t)f.batch * (size_t)f.context}, {a->dout, nb}};
+  for (size_t i = 0; i < 4; ++i) {
+    for (const auto& in : ins)
+      if (overlaps(outs[i].p, outs[i].n, in.p, in.n)) return AVEY_ERR_ALIAS;
+    for (size_t j = 0; j < i; ++j)
+      if (overlaps(outs[i].p, outs[i].n, outs[j].p, outs[j].n)) return AVEY_ERR_ALIAS;
+  }
+  if (p) {
+    *p = BwdParams{};
+    p->z = f.z_tr;
+    p->v = f.v;
+    p->gate = f.z_tl;
+    p->bias = f.bias;
+    p->valid = f.valid;
+    p->dout = a->dout;
+    p->dz = a->dz_tr;
+    p->dv = dv;
+    p->dgate = dg;
+    p->dbias = db;
+    p->B = f.batch;
+    p->C = f.context;
+    p->D = f.features;
+    p->causal = f.causal;
+    p->normalize = f.normalize;
+    p->act = f.activation;
+    p->eps = f.eps;
+    p->norm_eps = f.norm_eps;
+  }
+  return AVEY_OK;
+}
+}  // namespace
+
+int64_t avey_bwd_workspace_bytes(const avey_bwd_args* args) {
+  BwdParams p;
+  const int st = validate_bwd(args, &p);
+  if (st != AVEY_OK) return st;
+  return 4 * bwd_workspace_floats(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr);
+}
+
+int avey_bwd(const avey_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  BwdParams p;
+  const int st = validate_bwd(a, &p);
+  if (st != AVEY_OK) return st;
+  const size_t need = 4 * (size_t)bwd_workspace_floats(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255) != 0) return AVEY_ERR_WORKSPACE;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (!device_ok(dev)) return AVEY_ERR_DEVICE;
+  p.work = workspace;
+  e = launch_bwd(p, a->fwd.dtype, (hipStream_t)stream);
+  return e == hipSuccess ? AVEY_OK : (int)e;
+}
 
 int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   const int st = validate(a);

@@ -24,6 +24,30 @@ struct FwdParams {
   double eps, norm_eps;
 };
 
+// Arguments of the backward kernels. Every [B][C][D] operand is contiguous.
+struct BwdParams {
+  const void* z;        // z_tr
+  const void* v;        // [C][C] or null
+  const void* gate;     // z_tl or null
+  const void* bias;     // [D] or null
+  const uint8_t* valid; // [B][C] or null
+  const void* dout;     // incoming gradient [B][C][D]
+  void* dz;             // dz_tr [B][C][D]
+  void* dv;             // [C][C] or null (only with v)
+  void* dgate;          // dz_tl or null (only with gate)
+  void* dbias;          // [D] or null (only with bias)
+  void* work;           // bwd_workspace_floats(...) fp32 values
+  int64_t B, C, D;
+  int32_t causal, normalize, act;
+  double eps, norm_eps;
+};
+
+// Largest feature width of the backward kernels (16 accumulator tiles per wave).
+constexpr int64_t kBwdMaxFeatures = 1024;
+
+int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias);
+hipError_t launch_bwd(const BwdParams& p, int dtype, hipStream_t s);
+
 // Static tile table entry chosen on the host.
 struct Plan {
   int kernel;     // 1 fused MFMA, 2 generic

@@ -9,10 +9,11 @@ weights V shared across the batch (``ops.py:1-7``).
 
 Backends (``backend=``):
 
-* ``'auto'``   the fused HIP kernel for ROCm tensors on a gfx950 GPU when no
-  gradient is needed; otherwise the eager PyTorch path below (CPU tensors,
-  autograd, other GPUs) -- the same split the reference makes between its
-  fused kernel and ``_reference`` (``ops.py:96-106``). On a gfx950 device a
+* ``'auto'``   the fused HIP kernel for ROCm tensors on a gfx950 GPU, with the
+  fused HIP backward when gradients are needed (bf16 / fp16 / fp32 and at most
+  1024 features); otherwise the eager PyTorch path below (CPU tensors, other
+  GPUs, fp64 or wider rows under autograd). The reference sends every
+  gradient-requiring call to ``_reference`` (``ops.py:96-106``). On a gfx950 device a
   missing or broken ``libavey_hip.so`` raises instead of falling back.
 * ``'hip'``    the fused HIP kernel, or ``ValueError`` when it cannot run.
 * ``'triton'`` accepted for source compatibility: it names the reference's
@@ -137,10 +138,14 @@ def _dispatch(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, acti
     _validate(z_tr, v, z_tl, bias, valid, eps, norm_eps, activation, backend, output_tile, autotune)
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (z_tr, v, z_tl, bias))
-    fused_ok = _fused_device(z_tr) and not needs_grad
+    # With gradients the fused forward runs when the fused backward (avey_bwd) covers
+    # the inputs; otherwise autograd differentiates the eager path, which is what the
+    # reference always does for gradients (ops.py:96-106).
+    fused_ok = _fused_device(z_tr) and (not needs_grad or _hip.backward_supported(z_tr))
     if backend in ('hip', 'triton') and not fused_ok:
-        raise ValueError('the fused HIP kernel needs ROCm tensors on a gfx950 (MI355X) GPU and '
-                         'inference inputs; use backend="torch" for autograd or other devices')
+        raise ValueError('the fused HIP kernel needs ROCm tensors on a gfx950 (MI355X) GPU; with '
+                         'gradients also bf16 / fp16 / fp32 and at most 1024 features; use '
+                         'backend="torch" for other inputs')
     if backend == 'torch' or not fused_ok:
         return _eager(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation)
     # The fused path, one launch. z_tr / z_tl go in as they are when their features

@@ -14,7 +14,9 @@
  *                         static, documented tile table; host-only, no GPU needed.
  *   - avey_key_tile_count replaces `_key_tile_count` (avey_kernels/_triton.py:38-50),
  *                         the causal tile-skip rule; host-only.
- *   - avey_fwd_workspace_bytes, avey_status_string, avey_abi_version,
+ *   - avey_bwd            replaces autograd over the eager path for the
+ *                         gradients (avey_kernels/ops.py:96-106 and :61-91).
+ *   - avey_fwd_workspace_bytes, avey_bwd_workspace_bytes, avey_status_string, avey_abi_version,
  *     avey_device_supported: plumbing for the Python binding
  *     (avey_kernel_amd/_hip.py), no reference counterpart beyond the op's
  *     argument checks (avey_kernels/_triton.py:165-166).
@@ -43,7 +45,7 @@
 extern "C" {
 #endif
 
-#define AVEY_ABI_VERSION 2
+#define AVEY_ABI_VERSION 3
 
 /* Element type of z_tr / z_tl / v / bias / out. */
 enum avey_dtype {
@@ -74,6 +76,7 @@ enum avey_status {
   AVEY_ERR_FLAGS = -8,            /* causal / normalize not 0 or 1 */
   AVEY_ERR_ALIAS = -9,            /* out overlaps an input */
   AVEY_ERR_STRIDE = -10,          /* a row stride below features, or a negative stride */
+  AVEY_ERR_UNSUPPORTED = -11,     /* backward: fp64, features > 1024, batch > 65535 or strided operands */
 };
 
 typedef struct avey_fwd_args {
@@ -104,6 +107,18 @@ typedef struct avey_fwd_args {
   int64_t z_tl_batch_stride;
 } avey_fwd_args;
 
+/* Arguments of the backward (ABI 3). `fwd` holds the forward call's inputs and
+ * flags; fwd.out is ignored, and z_tr / z_tl must be contiguous (strides 0).
+ * dout and every gradient share fwd.dtype and the shape of their input. */
+typedef struct avey_bwd_args {
+  avey_fwd_args fwd;
+  const void* dout;     /* required: gradient of out, [batch][context][features] */
+  void* dz_tr;          /* required */
+  void* dv;             /* optional: [context][context]; NULL or fwd.v NULL: not computed */
+  void* dz_tl;          /* optional: NULL or fwd.z_tl NULL: not computed */
+  void* dbias;          /* optional: [features]; NULL or fwd.bias NULL: not computed */
+} avey_bwd_args;
+
 /* Kernel choice and launch geometry for one call; filled by avey_fwd_plan. */
 typedef struct avey_fwd_plan_t {
   int32_t kernel;        /* 1 = fused MFMA (bf16/fp16), 2 = generic VALU (fp32/fp64/wide) */
@@ -130,6 +145,19 @@ int avey_fwd_plan(const avey_fwd_args* args, avey_fwd_plan_t* plan);
  * diagonal tile). Host-only. Returns -1 on invalid input. */
 int64_t avey_key_tile_count(int64_t query_tile, int64_t context, int32_t block_m, int32_t block_n,
                             int32_t causal, int32_t skip);
+
+/* Gradients of the forward w.r.t. z_tr, v, z_tl and bias on `stream`. Replaces
+ * the reference's backward, which is PyTorch autograd over the eager path
+ * (avey_kernels/ops.py:96-106 selects it whenever an input requires grad; the
+ * math is ops.py:61-91) and materialises [batch, context, context] tensors; this
+ * one stores no context x context tile except the fp32 dv accumulator. bf16,
+ * fp16 and fp32; features <= 1024. Arithmetic in fp32. The workspace holds
+ * avey_bwd_workspace_bytes bytes; dv and dbias are summed with atomics, so their
+ * low bits may differ from call to call. */
+int avey_bwd(const avey_bwd_args* args, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device scratch bytes avey_bwd needs for these arguments, or a negative status. Host-only. */
+int64_t avey_bwd_workspace_bytes(const avey_bwd_args* args);
 
 /* 1 if `device` is a gfx950 GPU this library can run on, else 0. */
 int avey_device_supported(int device);

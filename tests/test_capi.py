@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_hip.EXPORTS), declared ^ set(_hip.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.avey_abi_version() == _hip.ABI_VERSION == 2
+    assert lib.avey_abi_version() == _hip.ABI_VERSION == 3
 
 
 def _args(**over):
@@ -70,6 +70,41 @@ def test_argument_errors_return_status_before_any_device_work(over, code):
     assert lib.avey_fwd_plan(ctypes.byref(args), ctypes.byref(_hip.AveyFwdPlan())) == code
     assert lib.avey_fwd_workspace_bytes(ctypes.byref(args)) == -1
     assert lib.avey_status_string(code).decode() not in ('', 'unknown status')
+
+
+def _bwd_args(dout=(1 << 42), dz_tr=(1 << 43), dv=None, dz_tl=None, dbias=None, **over):
+    return _hip.AveyBwdArgs(_args(**over), dout, dz_tr, dv, dz_tl, dbias)
+
+
+@pytest.mark.parametrize('over,code', [
+    (dict(dout=None), -1), (dict(dz_tr=None), -1), (dict(batch=0), -2), (dict(activation=7), -4),
+    (dict(dtype=3), -11), (dict(features=1025), -11), (dict(batch=65536), -11),
+    (dict(z_tr_row_stride=40, z_tr_batch_stride=35 * 40), -11),
+    (dict(dz_tr=(1 << 40) + 64), -9),              # dz_tr inside z_tr
+    (dict(dz_tr=(1 << 42) + 2), -9),               # dz_tr inside dout
+    (dict(z_tl=1 << 41, dz_tl=(1 << 43) + 8), -9),  # dz_tl overlaps dz_tr
+])
+def test_backward_argument_errors(over, code):
+    lib = _lib()
+    args = _bwd_args(**over)
+    assert lib.avey_bwd(ctypes.byref(args), None, 0, None) == code
+    assert lib.avey_bwd_workspace_bytes(ctypes.byref(args)) == code
+    assert lib.avey_status_string(code).decode() not in ('', 'unknown status')
+
+
+def test_backward_workspace_layout():
+    lib = _lib()
+    up = lambda n: -(-n // 64) * 64  # noqa: E731
+    b, c, d = 2, 35, 37
+    plain = lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args()))
+    assert plain == 4 * (2 * up(b * c) + 2 * up(b * c * d))
+    # dv and dbias accumulators only when both the input and its gradient are given.
+    assert lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args(dv=1 << 44))) == plain
+    full = _bwd_args(v=1 << 41, dv=1 << 44, bias=(1 << 41) + (1 << 30), dbias=1 << 45)
+    assert lib.avey_bwd_workspace_bytes(ctypes.byref(full)) == plain + 4 * (up(c * c) + up(d))
+    # The launch refuses a short or misaligned workspace before touching a device.
+    assert lib.avey_bwd(ctypes.byref(full), None, 0, None) == -6
+    assert lib.avey_bwd(ctypes.byref(full), (1 << 46) + 4, 1 << 30, None) == -6
 
 
 def test_null_args_pointer():

@@ -354,13 +354,20 @@ print('EQUAL' if torch.equal(out, ref) else 'DIFFER', flush=True)
     assert res.stdout.strip().endswith('EQUAL'), res.stdout[-500:]
 
 
-def test_gradient_request_falls_back_and_hip_backend_refuses():
-    z = torch.rand(2, 35, 37, device=DEV, requires_grad=True)
+def test_gradient_request_outside_the_fused_backward_falls_back_and_hip_backend_refuses():
+    # fp64 has no fused backward: 'auto' differentiates the eager path, 'hip' refuses.
+    z = torch.rand(2, 35, 37, device=DEV, dtype=torch.float64, requires_grad=True)
     out = avey_b(z)
     out.sum().backward()
     assert z.grad is not None and torch.isfinite(z.grad).all()
     with pytest.raises(ValueError):
         avey_b(z, backend='hip')
+    # Wider than 1024 features: the same.
+    zw = torch.rand(1, 8, 1040, device=DEV, requires_grad=True)
+    with pytest.raises(ValueError):
+        avey_b(zw, backend='hip')
+    avey_b(zw).sum().backward()
+    assert torch.isfinite(zw.grad).all()
 
 
 def test_hip_graph_replay_matches_eager():
