@@ -167,26 +167,54 @@ __device__ __forceinline__ float act_grad(float x, int act) {
 
 struct Ws {
   float *nrm, *dnum, *dden, *dzr, *dv, *db;
+  // bf16 path only: z transposed per batch item [D][cp] (padded rows zero),
+  // dnum in bf16 row-major [C][D] and transposed [D][cp].
+  __bf16 *zt, *dn16, *dnt;
+  int64_t cp;
 };
 
-// Workspace layout (fp32, each part 256-byte aligned): nrm [B*C], dden [B*C],
-// dnum [B*C*D], dzr [B*C*D], then dv [C*C] and dbias [D] when present.
+// Workspace layout (each part 256-byte aligned): nrm [B*C], dden [B*C], dzr
+// [B*C*D] fp32; then the fp32 path's dnum [B*C*D] fp32, or the bf16 path's zt
+// [B*D*cp], dn16 [B*C*D] and dnt [B*D*cp] bf16 (cp = C rounded up to 64); then
+// dv [C*C] and dbias [D] fp32 when present.
 __host__ __device__ inline int64_t up64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
-__host__ inline Ws carve(void* base, int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
-  float* p = (float*)base;
+__host__ inline int64_t ws_floats_parts(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast,
+                                        Ws* w, void* base) {
+  const int64_t cp = up64(C);
+  int64_t off = 0;
+  auto take = [&](int64_t n) { const int64_t o = off; off += up64(n); return o; };
+  const int64_t o_nrm = take(B * C), o_dden = take(B * C), o_dzr = take(B * C * D);
+  const int64_t o_dnum = fast ? -1 : take(B * C * D);
+  const int64_t o_zt = fast ? take((B * D * cp + 1) / 2) : -1;
+  const int64_t o_dn16 = fast ? take((B * C * D + 1) / 2) : -1;
+  const int64_t o_dnt = fast ? take((B * D * cp + 1) / 2) : -1;
+  const int64_t o_dv = has_v ? take(C * C) : -1;
+  const int64_t o_db = has_bias ? take(D) : -1;
+  if (w) {
+    float* f = (float*)base;
+    w->nrm = f + o_nrm;
+    w->dden = f + o_dden;
+    w->dzr = f + o_dzr;
+    w->dnum = o_dnum >= 0 ? f + o_dnum : nullptr;
+    w->zt = o_zt >= 0 ? (__bf16*)(f + o_zt) : nullptr;
+    w->dn16 = o_dn16 >= 0 ? (__bf16*)(f + o_dn16) : nullptr;
+    w->dnt = o_dnt >= 0 ? (__bf16*)(f + o_dnt) : nullptr;
+    w->dv = o_dv >= 0 ? f + o_dv : nullptr;
+    w->db = o_db >= 0 ? f + o_db : nullptr;
+    w->cp = cp;
+  }
+  return off;
+}
+
+__host__ inline Ws carve(void* base, int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
   Ws w;
-  w.nrm = p; p += up64(B * C);
-  w.dden = p; p += up64(B * C);
-  w.dnum = p; p += up64(B * C * D);
-  w.dzr = p; p += up64(B * C * D);
-  w.dv = has_v ? p : nullptr; p += has_v ? up64(C * C) : 0;
-  w.db = has_bias ? p : nullptr;
+  ws_floats_parts(B, C, D, has_v, has_bias, fast, &w, base);
   return w;
 }
 
-__host__ inline int64_t ws_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
-  return 2 * up64(B * C) + 2 * up64(B * C * D) + (has_v ? up64(C * C) : 0) + (has_bias ? up64(D) : 0);
+__host__ inline int64_t ws_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
+  return ws_floats_parts(B, C, D, has_v, has_bias, fast, nullptr, nullptr);
 }
 
 // One wave per row: ||z|| of the masked row. Every thread also clears a share of
@@ -502,9 +530,401 @@ __global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, Ws ws) {
     for (int64_t i = tid; i < p.D; i += nt) Io<T>::put((T*)p.dbias + i, ws.db[i]);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 path: 16x16x32 bf16 MFMA (fp32 accumulation) on bf16 operands, every
+// operand a 16-byte load. Products over features take z rows as stored (the
+// similarity is scaled by both inverse norms afterwards, so no operand is
+// re-rounded); products over rows take their right operand from transposed
+// copies (z^T, dnum^T) so that 8 consecutive rows of one column are adjacent.
+// dnum, P and dS are rounded to bf16 as MFMA operands; den, dden, dv, the
+// accumulators and the epilogues stay fp32. Needs D % 8 == 0 and a 16-byte
+// aligned z_tr.
+
+constexpr int kTp = kTile + 8;  // bf16 pitch of a [16][64] P / dS tile in LDS
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld8(const __bf16* p) { return *(const bf16x8*)p; }
+__device__ __forceinline__ bf16x8 zero8() { return __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u}); }
+
+// 16 x 16 block of A B^T over D features (A row lr = a, B row lr = b; a null row
+// is zero and not read). Lane group lg feeds features 32s + 8lg .. +7 at step s.
+// Loads of 8 steps are issued before their MFMAs. Result: lane holds C[4 lg + i][lr].
+__device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, int D, int lg) {
+  f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+  const int steps = (D + 31) >> 5;
+  for (int s0 = 0; s0 < steps; s0 += 8) {
+    bf16x8 x[8], y[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int d = 32 * (s0 + u) + 8 * lg;
+      const bool in = s0 + u < steps && d < D;
+      x[u] = (a && in) ? ld8(a + d) : zero8();
+      y[u] = (b && in) ? ld8(b + d) : zero8();
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u += 2) {
+      c0 = mfma16(x[u], y[u], c0);
+      c1 = mfma16(x[u + 1], y[u + 1], c1);
+    }
+  }
+  return c0 + c1;
+}
+
+// acc[t] (columns 16 (w + 4t) ..) += A (16 x 64 bf16 in LDS, pitch kTp) times
+// rows r0 .. r0+63 of Y, read from its transpose Yt [D][cp] (zero past the rows).
+template <int MAXT>
+__device__ __forceinline__ void rows_acc16(f32x4 (&acc)[MAXT], const __bf16* A, const __bf16* Yt, int64_t r0, int D,
+                                           int64_t cp, int w, int lr, int lg) {
+  const bf16x8 a0 = ld8(A + lr * kTp + 8 * lg);
+  const bf16x8 a1 = ld8(A + lr * kTp + 32 + 8 * lg);
+  const int ntiles = (D + 15) >> 4;
+  bf16x8 y0[MAXT], y1[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int col = 16 * (w + 4 * t) + lr;
+    const bool in = w + 4 * t < ntiles && col < D;
+    const __bf16* y = Yt + (int64_t)col * cp + r0 + 8 * lg;
+    y0[t] = in ? ld8(y) : zero8();
+    y1[t] = in ? ld8(y + 32) : zero8();
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    if (w + 4 * t >= ntiles) break;
+    acc[t] = mfma16(a0, y0[t], acc[t]);
+    acc[t] = mfma16(a1, y1[t], acc[t]);
+  }
+}
+
+// z^T per batch item into zt [D][cp] (padded and invalid rows zero), and zeros in
+// dnum^T's columns from C rounded up to 16 to cp (the rows kernel writes the rest).
+// One workgroup per (64 rows, 64 features) block through an LDS tile.
+__global__ __launch_bounds__(256) void bwd16_transpose_kernel(BwdParams p, Ws ws) {
+  __shared__ __bf16 tl[64][66];
+  const int64_t C = p.C, D = p.D, cp = ws.cp, b = blockIdx.z;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, d0 = (int64_t)blockIdx.y * 64;
+  const __bf16* zb = (const __bf16*)p.z + b * C * D;
+  for (int i = threadIdx.x; i < 512; i += 256) {
+    const int r = i >> 3, ch = (i & 7) * 8;
+    const int64_t c = c0 + r, d = d0 + ch;
+    bf16x8 x = zero8();
+    if (d < D && row_valid(p.valid, b, C, c)) x = ld8(zb + c * D + d);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tl[r][ch + e] = x[e];
+  }
+  __syncthreads();
+  const int64_t c16 = (C + 15) & ~int64_t(15);
+  for (int i = threadIdx.x; i < 512; i += 256) {
+    const int dd = i >> 3, ch = (i & 7) * 8;
+    const int64_t d = d0 + dd, c = c0 + ch;
+    if (d >= D) continue;
+    bf16x8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = tl[ch + e][dd];
+    *(bf16x8*)(ws.zt + (b * D + d) * cp + c) = x;
+    if (c >= c16) *(bf16x8*)(ws.dnt + (b * D + d) * cp + c) = zero8();
+  }
+}
+
+template <int MAXT>
+__global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
+  constexpr int dp = 64 * MAXT + 8;  // bf16 pitch of dnl; D <= 64 * MAXT
+  __shared__ __attribute__((aligned(16))) __bf16 tile[kRows * kTp];
+  __shared__ float red[4 * kRows];
+  __shared__ float stat[2 * kRows];
+  __shared__ __attribute__((aligned(16))) __bf16 dnl[kRows * dp];
+  const int D = (int)p.D;
+  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, q0 = (int64_t)blockIdx.x * kRows;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const float neps = (float)p.norm_eps;
+  const __bf16* zb = (const __bf16*)p.z + b * C * D;
+  const __bf16* ztb = ws.zt + b * D * cp;
+  const __bf16* vt = (const __bf16*)p.v;
+  const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
+  const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
+
+  const int64_t qa = q0 + lr;
+  const __bf16* qa_row = row_valid(p.valid, b, C, qa) ? zb + qa * D : nullptr;
+  float qinv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t q = q0 + 4 * lg + i;
+    qinv[i] = row_valid(p.valid, b, C, q) ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
+  }
+
+  // ---- pass 1: num, den ----
+  f32x4 acc[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float den4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k = kt * kTile + 16 * w + lr;
+    const bool k_ok = row_valid(p.valid, b, C, k);
+    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    const f32x4 s4 = row_dot16(qa_row, k_ok ? zb + k * D : nullptr, D, lg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      float pv = 0.f;
+      if (m) pv = s4[i] * qinv[i] * k_inv * (vt ? (float)vt[q * C + k] : 1.f);
+      den4[i] += pv;
+      tile[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)pv;
+    }
+    __syncthreads();
+    rows_acc16<MAXT>(acc, tile, ztb, kt * kTile, D, cp, w, lr, lg);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(den4[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    stat[i] = red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i] + (float)p.eps;
+  }
+  __syncthreads();
+
+  // ---- epilogue 1: dz_tl, dnum (LDS, row-major and transposed bf16), dden, dbias ----
+  const int ntiles = (D + 15) >> 4;
+  float ddp[4] = {0.f, 0.f, 0.f, 0.f};
+  const __bf16* gb = p.gate ? (const __bf16*)p.gate + b * C * D : nullptr;
+  const __bf16* ob = (const __bf16*)p.dout + b * C * D;
+  __bf16* dgb = p.dgate ? (__bf16*)p.dgate + b * C * D : nullptr;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+    float dbs = 0.f;
+    bf16x4 dn4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * lg + i;
+      const int64_t q = q0 + row;
+      float dn = 0.f;
+      if (col < D && q < C) {
+        const bool rq = row_valid(p.valid, b, C, q);
+        const float den = stat[row];
+        const float y = p.normalize ? acc[t][i] / den : acc[t][i];
+        const float u = y + (p.bias ? (float)((const __bf16*)p.bias)[col] : 0.f);
+        const float go = rq ? (float)ob[q * D + col] : 0.f;
+        const float gt = gb ? (rq ? (float)gb[q * D + col] : 0.f) : 1.f;
+        if (dgb) dgb[q * D + col] = (__bf16)(go * activate<float>(u, p.act));
+        const float du = go * gt * act_grad(u, p.act);
+        dbs += du;
+        dn = p.normalize ? du / den : du;
+        ddp[i] += du * y;
+        ws.dn16[(b * C + q) * D + col] = (__bf16)dn;
+      }
+      dn4[i] = (__bf16)dn;
+      dnl[row * dp + col] = dn4[i];
+    }
+    if (col < D) *(bf16x4*)(ws.dnt + (b * D + col) * cp + q0 + 4 * lg) = dn4;
+    if (ws.db) {
+      dbs += __shfl_xor(dbs, 16);
+      dbs += __shfl_xor(dbs, 32);
+      if (lg == 0 && col < D) unsafeAtomicAdd(ws.db + col, dbs);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(ddp[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    const int64_t q = q0 + i;
+    float dd = 0.f;
+    if (p.normalize) dd = -(red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / stat[i];
+    stat[kRows + i] = dd;
+    if (q < C) ws.dden[b * C + q] = dd;
+  }
+  __syncthreads();
+
+  // ---- pass 2: dP, dS, dv, dS zhat ----
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const __bf16* dn_row = dnl + lr * dp;
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k = kt * kTile + 16 * w + lr;
+    const bool k_ok = row_valid(p.valid, b, C, k);
+    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    const __bf16* k_row = k_ok ? zb + k * D : nullptr;
+    const f32x4 s4 = row_dot16(qa_row, k_row, D, lg);
+    const f32x4 d4 = row_dot16(dn_row, k_row, D, lg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      float dsv = 0.f;
+      if (m) {
+        const float dpv = d4[i] + stat[kRows + 4 * lg + i];
+        const float vv = vt ? (float)vt[q * C + k] : 1.f;
+        dsv = dpv * vv * k_inv;
+        if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i] * qinv[i] * k_inv);
+      }
+      tile[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)dsv;
+    }
+    __syncthreads();
+    rows_acc16<MAXT>(acc, tile, ztb, kt * kTile, D, cp, w, lr, lg);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      if (col < D && q < C) ws.dzr[(b * C + q) * D + col] = acc[t][i];
+    }
+  }
+}
+
+template <int MAXT>
+__global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
+  __shared__ __attribute__((aligned(16))) __bf16 pt[kRows * kTp];  // P^T [16 keys][64 queries]
+  __shared__ __attribute__((aligned(16))) __bf16 dt[kRows * kTp];  // (dS * inv(query))^T
+  __shared__ float red[4 * kRows];
+  __shared__ float rad[kRows];
+  const int D = (int)p.D;
+  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, k0 = (int64_t)blockIdx.x * kRows;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const float neps = (float)p.norm_eps;
+  const __bf16* zb = (const __bf16*)p.z + b * C * D;
+  const __bf16* ztb = ws.zt + b * D * cp;
+  const __bf16* dnb = ws.dn16 + b * C * D;
+  const __bf16* dntb = ws.dnt + b * D * cp;
+  const __bf16* vt = (const __bf16*)p.v;
+
+  const int64_t ka = k0 + lr;
+  const __bf16* ka_row = row_valid(p.valid, b, C, ka) ? zb + ka * D : nullptr;
+  float kinv[4];
+  bool kok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t k = k0 + 4 * lg + i;
+    kok[i] = row_valid(p.valid, b, C, k);
+    kinv[i] = kok[i] ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+  }
+
+  f32x4 acc1[MAXT], acc2[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Query tiles start at multiples of 64 so that the 64 rows each one reads from
+  // the transposed copies stay inside their cp (a multiple of 64) columns.
+  const int64_t qstart = p.causal ? (k0 / kTile) * kTile : 0;
+  for (int64_t qt = qstart; qt < C; qt += kTile) {
+    const int64_t q = qt + 16 * w + lr;
+    const bool q_in = q < C;
+    const bool q_ok = row_valid(p.valid, b, C, q);
+    const float q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
+    const f32x4 s4 = row_dot16(ka_row, q_ok ? zb + q * D : nullptr, D, lg);
+    const f32x4 d4 = row_dot16(ka_row, q_in ? dnb + q * D : nullptr, D, lg);
+    const float dd = q_in ? ws.dden[b * C + q] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      const bool m = q_in && kok[i] && (!p.causal || k <= q);
+      float pv = 0.f, dsv = 0.f;
+      if (m) {
+        const float vv = vt ? (float)vt[q * C + k] : 1.f;
+        pv = s4[i] * kinv[i] * q_inv * vv;
+        dsv = (d4[i] + dd) * vv * q_inv;
+      }
+      pt[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)pv;
+      dt[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)dsv;
+    }
+    __syncthreads();
+    rows_acc16<MAXT>(acc1, pt, dntb, qt, D, cp, w, lr, lg);
+    rows_acc16<MAXT>(acc2, dt, ztb, qt, D, cp, w, lr, lg);
+    __syncthreads();
+  }
+
+  const int ntiles = (D + 15) >> 4;
+  float rp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      if (col < D && kok[i]) {
+        const float g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
+        acc2[t][i] = g;
+        rp[i] += (float)zb[k * D + col] * g;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = sum16(rp[i]);
+    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRows) {
+    const int i = threadIdx.x;
+    const int64_t k = k0 + i;
+    float r = 0.f;
+    if (row_valid(p.valid, b, C, k)) {
+      const float n = ws.nrm[b * C + k];
+      if (n >= neps) r = (red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / n;
+    }
+    rad[i] = r;
+  }
+  __syncthreads();
+  __bf16* dzb = (__bf16*)p.dz + b * C * D;
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int tile_i = w + 4 * t;
+    if (tile_i >= ntiles) break;
+    const int col = 16 * tile_i + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      if (col >= D || k >= C) continue;
+      float g = 0.f;
+      if (kok[i]) {
+        const float zh = (float)zb[k * D + col] * kinv[i];
+        g = acc1[t][i] + (acc2[t][i] - zh * rad[4 * lg + i]) * kinv[i];
+      }
+      dzb[k * D + col] = (__bf16)g;
+    }
+  }
+}
+
+template <int MAXT>
+hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
+  Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, true);
+  const int64_t rows = p.B * p.C;
+  hipLaunchKernelGGL(bwd_prep_kernel<__bf16>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL(bwd16_transpose_kernel, dim3((unsigned)(ws.cp / 64), (unsigned)cdiv(p.D, 64), (unsigned)p.B),
+                     dim3(256), 0, s, p, ws);
+  const dim3 grid((unsigned)cdiv(p.C, kRows), (unsigned)p.B);
+  hipLaunchKernelGGL((bwd16_rows_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd16_cols_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
+  if (p.dv || p.dbias) {
+    const int64_t n = p.dv ? p.C * p.C : p.D;
+    const int64_t blocks = cdiv(n, 256) < 1024 ? cdiv(n, 256) : 1024;
+    hipLaunchKernelGGL(bwd_final_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
+  }
+  return hipGetLastError();
+}
+
 template <typename T, int MAXT>
 hipError_t launch_bwd_t(const BwdParams& p, hipStream_t s) {
-  Ws ws = carve(p.work, p.B, p.C, p.D, p.v != nullptr, p.bias != nullptr);
+  Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, false);
   const int64_t rows = p.B * p.C;
   hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
   const dim3 grid((unsigned)cdiv(p.C, kRows), (unsigned)p.B);
@@ -527,13 +947,26 @@ hipError_t launch_bwd_d(const BwdParams& p, hipStream_t s) {
   return launch_bwd_t<T, 16>(p, s);
 }
 
+hipError_t launch_bwd16(const BwdParams& p, hipStream_t s) {
+  const int64_t tiles = cdiv(p.D, 16);
+  if (tiles <= 8) return launch_bwd16_t<2>(p, s);
+  if (tiles <= 16) return launch_bwd16_t<4>(p, s);
+  if (tiles <= 32) return launch_bwd16_t<8>(p, s);
+  return launch_bwd16_t<16>(p, s);
+}
+
 }  // namespace
 
-int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias) {
-  return ws_floats(B, C, D, has_v, has_bias);
+bool bwd_fast_path(int dtype, int64_t D, const void* z) {
+  return dtype == AVEY_DTYPE_BF16 && D % 8 == 0 && ((uintptr_t)z & 15) == 0;
+}
+
+int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
+  return ws_floats(B, C, D, has_v, has_bias, fast);
 }
 
 hipError_t launch_bwd(const BwdParams& p, int dtype, hipStream_t s) {
+  if (bwd_fast_path(dtype, p.D, p.z)) return launch_bwd16(p, s);
   switch (dtype) {
     case AVEY_DTYPE_BF16: return launch_bwd_d<__bf16>(p, s);
     case AVEY_DTYPE_F16: return launch_bwd_d<_Float16>(p, s);

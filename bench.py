@@ -52,6 +52,9 @@ def parse_args():
                          'after one plain copy of --copy-mib MiB, whose HBM counters calibrate the '
                          'per-dispatch FETCH_SIZE / WRITE_SIZE readings')
     ap.add_argument('--copy-mib', type=int, default=256)
+    ap.add_argument('--backward', action='store_true',
+                    help='also time the fused backward (avey_bwd) and forward+backward through autograd '
+                         'against autograd over the eager path, for every configuration')
     return ap.parse_args()
 
 
@@ -165,6 +168,53 @@ def measure_config(torch, wl, tag, steps, warmup, cold_calls):
     return cfg, inp, flops, nbytes, per_call_ms, wall_ms, eager_ms, cold_ms
 
 
+def measure_backward(torch, wl, tag, steps, warmup):
+    """Fused backward alone (HIP graph), and forward + backward through autograd for
+    the fused op and for the eager path (the reference's gradient path, ops.py:96-106)."""
+    cfg = wl.CONFIGS[tag]
+    inp = wl.make_inputs(cfg, device='cuda')
+    g = torch.Generator().manual_seed(100 + cfg.seed)
+    dout = torch.randn(inp['z_tr'].shape, generator=g).to(cfg.dtype).to('cuda')
+    v = inp['v'] if cfg.op == 'avey' else None
+    normalize = cfg.op == 'avey_b'
+    op = torch.ops.avey_kernels.contextualize_backward
+
+    def bwd():
+        return op(dout, inp['z_tr'], v, inp['z_tl'], inp['bias'], inp['valid'], 1e-6, 1e-12, cfg.causal, normalize,
+                  'identity', True, True, True)
+
+    bwd_ms, _ = measure_graph(torch, bwd, steps, warmup)
+    leaves = {k: (t.clone().requires_grad_() if k in ('z_tr', 'z_tl', 'v', 'bias') else t) for k, t in inp.items()}
+
+    def fwd_bwd(backend):
+        def run():
+            for t in leaves.values():
+                if t is not None and t.requires_grad:
+                    t.grad = None
+            wl.call(cfg, leaves, backend=backend).backward(dout)
+        return run
+
+    fused = fwd_bwd('hip')
+    eager = fwd_bwd('torch')
+    for fn in (fused, eager):
+        for _ in range(3):
+            fn()
+    reps = max(steps // 4, 10)
+    fused_ms = measure_eager(torch, fused, reps)
+    eager_ms = measure_eager(torch, eager, reps)
+    # Useful backward work: S, num, dP, dS zhat, dS^T zhat and P^T dnum once each,
+    # 2 * D flops per allowed pair apiece (the kernels recompute S and num on top).
+    flops = 3 * wl.useful_flops(cfg, inp['valid'])
+    row = {'config': cfg.name, 'bwd_us': round(bwd_ms * 1e3, 2),
+           'bwd_tflops_useful': round(flops / (bwd_ms * 1e-3) / 1e12, 2),
+           'fwd_bwd_autograd_us_fused': round(fused_ms * 1e3, 1),
+           'fwd_bwd_autograd_us_eager': round(eager_ms * 1e3, 1),
+           'speedup_vs_eager': round(eager_ms / fused_ms, 2)}
+    del inp, leaves
+    torch.cuda.empty_cache()
+    return row
+
+
 def roofline_block(flops, nbytes, per_call_ms, traffic):
     ai = flops / nbytes
     if ai < RIDGE:
@@ -275,6 +325,13 @@ def main():
             del i2
             torch.cuda.empty_cache()
 
+    bwd_rows = []
+    if args.backward:
+        for tag in wl.CONFIGS:
+            row = measure_backward(torch, wl, tag, max(args.steps // 4, 20), min(args.warmup, 5))
+            bwd_rows.append(row)
+            log(f'[bench] backward {json.dumps(row)}')
+
     line = {
         'metric': METRIC,
         'value': round(tflops, 3),
@@ -302,7 +359,7 @@ def main():
     }
     if args.report:
         with open(args.report, 'w') as fh:
-            json.dump({'headline': line, 'configs': all_rows}, fh, indent=1)
+            json.dump({'headline': line, 'configs': all_rows, 'backward': bwd_rows}, fh, indent=1)
     print(json.dumps(line), flush=True)
 
 
