@@ -252,7 +252,8 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
   __shared__ float stat[2 * kRows];          // den, dden of the block's rows
   __shared__ __attribute__((aligned(16))) float dnl[kRows * dp];  // dnum of the block's rows
   const int D = (int)p.D;
-  const int64_t C = p.C, b = blockIdx.y, q0 = (int64_t)blockIdx.x * kRows;
+  // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
+  const int64_t C = p.C, b = blockIdx.y, q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const bool vec = (D & 3) == 0;
@@ -573,6 +574,56 @@ __device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, int
   return c0 + c1;
 }
 
+// Two row dots sharing an operand: c1 = a1 b^T and c2 = a2 b^T (b loaded once), or
+// with `shared_a`, c1 = a b1^T and c2 = a b2^T (a loaded once). Same lane layout
+// as row_dot16; a null row is zero and not read.
+template <bool shared_a>
+__device__ __forceinline__ void row_dot16x2(const __bf16* a1, const __bf16* a2, const __bf16* b1, const __bf16* b2,
+                                            int D, int lg, f32x4& c1, f32x4& c2) {
+  c1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int steps = (D + 31) >> 5;
+  for (int s0 = 0; s0 < steps; s0 += 4) {
+    bf16x8 x1[4], x2[4], y1[4], y2[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = 32 * (s0 + u) + 8 * lg;
+      const bool in = s0 + u < steps && d < D;
+      if (shared_a) {
+        x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
+        y1[u] = (b1 && in) ? ld8(b1 + d) : zero8();
+        y2[u] = (b2 && in) ? ld8(b2 + d) : zero8();
+      } else {
+        x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
+        x2[u] = (a2 && in) ? ld8(a2 + d) : zero8();
+        y1[u] = (b1 && in) ? ld8(b1 + d) : zero8();
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (shared_a) {
+        c1 = mfma16(x1[u], y1[u], c1);
+        c2 = mfma16(x1[u], y2[u], c2);
+      } else {
+        c1 = mfma16(x1[u], y1[u], c1);
+        c2 = mfma16(x2[u], y1[u], c2);
+      }
+    }
+  }
+}
+
+// Copies rows r0 .. r0+15 of z (features contiguous) into LDS rows of pitch `pitch`
+// bf16, zero for padded or out-of-range rows. D % 8 == 0.
+__device__ __forceinline__ void stage_rows16(__bf16* dst, int pitch, const __bf16* zb, const uint8_t* valid, int64_t b,
+                                             int64_t C, int64_t r0, int D) {
+  const int chunks = D >> 3;
+  for (int i = threadIdx.x; i < kRows * chunks; i += blockDim.x) {
+    const int r = i / chunks, c = (i - r * chunks) * 8;
+    const int64_t row = r0 + r;
+    *(bf16x8*)(dst + r * pitch + c) = row_valid(valid, b, C, row) ? ld8(zb + row * D + c) : zero8();
+  }
+}
+
 // acc[t] (columns 16 (w + 4t) ..) += A (16 x 64 bf16 in LDS, pitch kTp) times
 // rows r0 .. r0+63 of Y, read from its transpose Yt [D][cp] (zero past the rows).
 template <int MAXT>
@@ -635,8 +686,10 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   __shared__ float red[4 * kRows];
   __shared__ float stat[2 * kRows];
   __shared__ __attribute__((aligned(16))) __bf16 dnl[kRows * dp];
+  __shared__ __attribute__((aligned(16))) __bf16 qzl[kRows * dp];  // the block's query rows
   const int D = (int)p.D;
-  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, q0 = (int64_t)blockIdx.x * kRows;
+  // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
+  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const float neps = (float)p.norm_eps;
@@ -646,14 +699,16 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
   const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
 
-  const int64_t qa = q0 + lr;
-  const __bf16* qa_row = row_valid(p.valid, b, C, qa) ? zb + qa * D : nullptr;
+  stage_rows16(qzl, dp, zb, p.valid, b, C, q0, D);
+  const __bf16* qa_row = qzl + lr * dp;  // A rows of the row dots (zero when padded)
   float qinv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t q = q0 + 4 * lg + i;
     qinv[i] = row_valid(p.valid, b, C, q) ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
   }
+
+  __syncthreads();
 
   // ---- pass 1: num, den ----
   f32x4 acc[MAXT];
@@ -757,8 +812,8 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
     const __bf16* k_row = k_ok ? zb + k * D : nullptr;
-    const f32x4 s4 = row_dot16(qa_row, k_row, D, lg);
-    const f32x4 d4 = row_dot16(dn_row, k_row, D, lg);
+    f32x4 s4, d4;
+    row_dot16x2<false>(qa_row, dn_row, k_row, nullptr, D, lg, s4, d4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
@@ -795,6 +850,8 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   __shared__ __attribute__((aligned(16))) __bf16 dt[kRows * kTp];  // (dS * inv(query))^T
   __shared__ float red[4 * kRows];
   __shared__ float rad[kRows];
+  constexpr int dp = 64 * MAXT + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 kzl[kRows * dp];  // the block's key rows
   const int D = (int)p.D;
   const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, k0 = (int64_t)blockIdx.x * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -806,8 +863,8 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   const __bf16* dntb = ws.dnt + b * D * cp;
   const __bf16* vt = (const __bf16*)p.v;
 
-  const int64_t ka = k0 + lr;
-  const __bf16* ka_row = row_valid(p.valid, b, C, ka) ? zb + ka * D : nullptr;
+  stage_rows16(kzl, dp, zb, p.valid, b, C, k0, D);
+  const __bf16* ka_row = kzl + lr * dp;  // A rows of the row dots (zero when padded)
   float kinv[4];
   bool kok[4];
 #pragma unroll
@@ -817,6 +874,7 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
     kinv[i] = kok[i] ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
   }
 
+  __syncthreads();
   f32x4 acc1[MAXT], acc2[MAXT];
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -828,8 +886,8 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
     const float q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
-    const f32x4 s4 = row_dot16(ka_row, q_ok ? zb + q * D : nullptr, D, lg);
-    const f32x4 d4 = row_dot16(ka_row, q_in ? dnb + q * D : nullptr, D, lg);
+    f32x4 s4, d4;
+    row_dot16x2<true>(ka_row, nullptr, q_ok ? zb + q * D : nullptr, q_in ? dnb + q * D : nullptr, D, lg, s4, d4);
     const float dd = q_in ? ws.dden[b * C + q] : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
