@@ -165,6 +165,24 @@ __device__ __forceinline__ float act_grad(float x, int act) {
   }
 }
 
+// (batch item, row tile) of this workgroup in a 1-D grid of B * nt workgroups.
+// Workgroups are dealt to the 8 XCDs round-robin by linear id, so ids are mapped
+// such that the tiles of one batch item run on one XCD (B a multiple of 8) or on
+// 8 / B of them (B divides 8), and that batch item's rows stay in those XCDs' L2.
+// `heavy_last`: tiles are visited last-first (causal query tiles grow heavier).
+__device__ __forceinline__ void tile_of_block(int64_t B, int64_t nt, bool heavy_last, int64_t& b, int64_t& t) {
+  const int64_t L = blockIdx.x;
+  if (B % 8 == 0) {
+    const int64_t slot = L >> 3;
+    b = (L & 7) + 8 * (slot / nt);
+    t = slot % nt;
+  } else {
+    b = L % B;
+    t = L / B;
+  }
+  if (heavy_last) t = nt - 1 - t;
+}
+
 struct Ws {
   float *nrm, *dnum, *dden, *dzr, *dv, *db;
   // bf16 path only: z transposed per batch item [D][cp] (padded rows zero),
@@ -253,7 +271,10 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
   __shared__ __attribute__((aligned(16))) float dnl[kRows * dp];  // dnum of the block's rows
   const int D = (int)p.D;
   // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
-  const int64_t C = p.C, b = blockIdx.y, q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kRows;
+  const int64_t C = p.C;
+  int64_t b, qtile;
+  tile_of_block(p.B, cdiv(C, kRows), true, b, qtile);
+  const int64_t q0 = qtile * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const bool vec = (D & 3) == 0;
@@ -413,7 +434,10 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
   __shared__ float red[4 * kRows];
   __shared__ float rad[kRows];
   const int D = (int)p.D;
-  const int64_t C = p.C, b = blockIdx.y, k0 = (int64_t)blockIdx.x * kRows;
+  const int64_t C = p.C;
+  int64_t b, ktile;
+  tile_of_block(p.B, cdiv(C, kRows), false, b, ktile);  // causal: the first key tiles are the heaviest
+  const int64_t k0 = ktile * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const bool vec = (D & 3) == 0;
@@ -689,7 +713,10 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   __shared__ __attribute__((aligned(16))) __bf16 qzl[kRows * dp];  // the block's query rows
   const int D = (int)p.D;
   // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
-  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kRows;
+  const int64_t C = p.C, cp = ws.cp;
+  int64_t b, qtile;
+  tile_of_block(p.B, cdiv(C, kRows), true, b, qtile);
+  const int64_t q0 = qtile * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const float neps = (float)p.norm_eps;
@@ -853,7 +880,10 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   constexpr int dp = 64 * MAXT + 8;
   __shared__ __attribute__((aligned(16))) __bf16 kzl[kRows * dp];  // the block's key rows
   const int D = (int)p.D;
-  const int64_t C = p.C, cp = ws.cp, b = blockIdx.y, k0 = (int64_t)blockIdx.x * kRows;
+  const int64_t C = p.C, cp = ws.cp;
+  int64_t b, ktile;
+  tile_of_block(p.B, cdiv(C, kRows), false, b, ktile);  // causal: the first key tiles are the heaviest
+  const int64_t k0 = ktile * kRows;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const float neps = (float)p.norm_eps;
@@ -969,7 +999,7 @@ hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL(bwd_prep_kernel<__bf16>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
   hipLaunchKernelGGL(bwd16_transpose_kernel, dim3((unsigned)(ws.cp / 64), (unsigned)cdiv(p.D, 64), (unsigned)p.B),
                      dim3(256), 0, s, p, ws);
-  const dim3 grid((unsigned)cdiv(p.C, kRows), (unsigned)p.B);
+  const dim3 grid((unsigned)(cdiv(p.C, kRows) * p.B));  // 1-D, mapped by tile_of_block
   hipLaunchKernelGGL((bwd16_rows_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
   hipLaunchKernelGGL((bwd16_cols_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
   if (p.dv || p.dbias) {
@@ -985,7 +1015,7 @@ hipError_t launch_bwd_t(const BwdParams& p, hipStream_t s) {
   Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, false);
   const int64_t rows = p.B * p.C;
   hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
-  const dim3 grid((unsigned)cdiv(p.C, kRows), (unsigned)p.B);
+  const dim3 grid((unsigned)(cdiv(p.C, kRows) * p.B));  // 1-D, mapped by tile_of_block
   hipLaunchKernelGGL((bwd_rows_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
   hipLaunchKernelGGL((bwd_cols_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
   if (p.dv || p.dbias) {
