@@ -193,13 +193,13 @@ struct Ws {
 
 // Workspace layout (each part 256-byte aligned): nrm [B*C], dden [B*C], dzr
 // [B*C*D] fp32; then the fp32 path's dnum [B*C*D] fp32, or the bf16 path's zt
-// [B*D*cp], dn16 [B*C*D] and dnt [B*D*cp] bf16 (cp = C rounded up to 64); then
+// [B*D*cp], dn16 [B*C*D] and dnt [B*D*cp] bf16 (cp = C rounded up to 128); then
 // dv [C*C] and dbias [D] fp32 when present.
 __host__ __device__ inline int64_t up64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
 __host__ inline int64_t ws_floats_parts(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast,
                                         Ws* w, void* base) {
-  const int64_t cp = up64(C);
+  const int64_t cp = (C + 127) & ~int64_t(127);  // a multiple of the bf16 kernels' 128-row tiles
   int64_t off = 0;
   auto take = [&](int64_t n) { const int64_t o = off; off += up64(n); return o; };
   const int64_t o_nrm = take(B * C), o_dden = take(B * C), o_dzr = take(B * C * D);
@@ -565,7 +565,16 @@ __global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, Ws ws) {
 // accumulators and the epilogues stay fp32. Needs D % 8 == 0 and a 16-byte
 // aligned z_tr.
 
-constexpr int kTp = kTile + 8;  // bf16 pitch of a [16][64] P / dS tile in LDS
+// The bf16 kernels run NW waves per workgroup: row tiles of KT = 16 NW rows on the
+// other side, a [16][KT] P / dS tile in LDS (pitch KT + 8 bf16), and wave w owning
+// the 16-column tiles w, w + NW, w + 2 NW, ... of the [16, D] accumulators.
+template <int NW>
+__device__ __forceinline__ float sum_waves(const float* red, int i) {
+  float x = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) x += red[w * kRows + i];
+  return x;
+}
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -648,28 +657,37 @@ __device__ __forceinline__ void stage_rows16(__bf16* dst, int pitch, const __bf1
   }
 }
 
-// acc[t] (columns 16 (w + 4t) ..) += A (16 x 64 bf16 in LDS, pitch kTp) times
-// rows r0 .. r0+63 of Y, read from its transpose Yt [D][cp] (zero past the rows).
-template <int MAXT>
+// acc[t] (columns 16 (w + NW t) ..) += A (16 x KT bf16 in LDS, pitch KT + 8) times
+// rows r0 .. r0+KT-1 of Y, read from its transpose Yt [D][cp] (zero past the rows).
+// Operands of up to 4 column tiles are in flight at a time.
+template <int NW, int MAXT>
 __device__ __forceinline__ void rows_acc16(f32x4 (&acc)[MAXT], const __bf16* A, const __bf16* Yt, int64_t r0, int D,
                                            int64_t cp, int w, int lr, int lg) {
-  const bf16x8 a0 = ld8(A + lr * kTp + 8 * lg);
-  const bf16x8 a1 = ld8(A + lr * kTp + 32 + 8 * lg);
+  constexpr int KS = NW / 2;  // 32-row MFMA steps per tile
+  constexpr int TP = 16 * NW + 8;
+  constexpr int G = MAXT < 4 ? MAXT : 4;
+  bf16x8 a[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) a[k] = ld8(A + lr * TP + 32 * k + 8 * lg);
   const int ntiles = (D + 15) >> 4;
-  bf16x8 y0[MAXT], y1[MAXT];
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    const int col = 16 * (w + 4 * t) + lr;
-    const bool in = w + 4 * t < ntiles && col < D;
-    const __bf16* y = Yt + (int64_t)col * cp + r0 + 8 * lg;
-    y0[t] = in ? ld8(y) : zero8();
-    y1[t] = in ? ld8(y + 32) : zero8();
-  }
+  for (int t0 = 0; t0 < MAXT; t0 += G) {
+    if (w + NW * t0 >= ntiles) break;
+    bf16x8 y[G][KS];
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    if (w + 4 * t >= ntiles) break;
-    acc[t] = mfma16(a0, y0[t], acc[t]);
-    acc[t] = mfma16(a1, y1[t], acc[t]);
+    for (int t = 0; t < G; ++t) {
+      const int col = 16 * (w + NW * (t0 + t)) + lr;
+      const bool in = w + NW * (t0 + t) < ntiles && col < D;
+      const __bf16* yp = Yt + (int64_t)col * cp + r0 + 8 * lg;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) y[t][k] = in ? ld8(yp + 32 * k) : zero8();
+    }
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      if (w + NW * (t0 + t) >= ntiles) break;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) acc[t0 + t] = mfma16(a[k], y[t][k], acc[t0 + t]);
+    }
   }
 }
 
@@ -703,11 +721,12 @@ __global__ __launch_bounds__(256) void bwd16_transpose_kernel(BwdParams p, Ws ws
   }
 }
 
-template <int MAXT>
-__global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
-  constexpr int dp = 64 * MAXT + 8;  // bf16 pitch of dnl; D <= 64 * MAXT
-  __shared__ __attribute__((aligned(16))) __bf16 tile[kRows * kTp];
-  __shared__ float red[4 * kRows];
+template <int NW, int MAXT>
+__global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws) {
+  constexpr int KT = 16 * NW, TP = KT + 8;
+  constexpr int dp = 16 * NW * MAXT + 8;  // bf16 pitch of dnl; D <= 16 NW MAXT
+  __shared__ __attribute__((aligned(16))) __bf16 tile[kRows * TP];
+  __shared__ float red[NW * kRows];
   __shared__ float stat[2 * kRows];
   __shared__ __attribute__((aligned(16))) __bf16 dnl[kRows * dp];
   __shared__ __attribute__((aligned(16))) __bf16 qzl[kRows * dp];  // the block's query rows
@@ -724,7 +743,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   const __bf16* ztb = ws.zt + b * D * cp;
   const __bf16* vt = (const __bf16*)p.v;
   const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
-  const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
+  const int64_t nkt = p.causal ? cdiv(qend, KT) : cdiv(C, KT);
 
   stage_rows16(qzl, dp, zb, p.valid, b, C, q0, D);
   const __bf16* qa_row = qzl + lr * dp;  // A rows of the row dots (zero when padded)
@@ -743,7 +762,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float den4[4] = {0.f, 0.f, 0.f, 0.f};
   for (int64_t kt = 0; kt < nkt; ++kt) {
-    const int64_t k = kt * kTile + 16 * w + lr;
+    const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
     const f32x4 s4 = row_dot16(qa_row, k_ok ? zb + k * D : nullptr, D, lg);
@@ -754,10 +773,10 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
       float pv = 0.f;
       if (m) pv = s4[i] * qinv[i] * k_inv * (vt ? (float)vt[q * C + k] : 1.f);
       den4[i] += pv;
-      tile[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)pv;
+      tile[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)pv;
     }
     __syncthreads();
-    rows_acc16<MAXT>(acc, tile, ztb, kt * kTile, D, cp, w, lr, lg);
+    rows_acc16<NW, MAXT>(acc, tile, ztb, kt * KT, D, cp, w, lr, lg);
     __syncthreads();
   }
 #pragma unroll
@@ -768,7 +787,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   __syncthreads();
   if (threadIdx.x < kRows) {
     const int i = threadIdx.x;
-    stat[i] = red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i] + (float)p.eps;
+    stat[i] = sum_waves<NW>(red, i) + (float)p.eps;
   }
   __syncthreads();
 
@@ -780,7 +799,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   __bf16* dgb = p.dgate ? (__bf16*)p.dgate + b * C * D : nullptr;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
+    const int tile_i = w + NW * t;
     if (tile_i >= ntiles) break;
     const int col = 16 * tile_i + lr;
     float dbs = 0.f;
@@ -824,7 +843,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
     const int i = threadIdx.x;
     const int64_t q = q0 + i;
     float dd = 0.f;
-    if (p.normalize) dd = -(red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / stat[i];
+    if (p.normalize) dd = -(sum_waves<NW>(red, i)) / stat[i];
     stat[kRows + i] = dd;
     if (q < C) ws.dden[b * C + q] = dd;
   }
@@ -835,7 +854,7 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const __bf16* dn_row = dnl + lr * dp;
   for (int64_t kt = 0; kt < nkt; ++kt) {
-    const int64_t k = kt * kTile + 16 * w + lr;
+    const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
     const __bf16* k_row = k_ok ? zb + k * D : nullptr;
@@ -852,15 +871,15 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
         dsv = dpv * vv * k_inv;
         if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i] * qinv[i] * k_inv);
       }
-      tile[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)dsv;
+      tile[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)dsv;
     }
     __syncthreads();
-    rows_acc16<MAXT>(acc, tile, ztb, kt * kTile, D, cp, w, lr, lg);
+    rows_acc16<NW, MAXT>(acc, tile, ztb, kt * KT, D, cp, w, lr, lg);
     __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
+    const int tile_i = w + NW * t;
     if (tile_i >= ntiles) break;
     const int col = 16 * tile_i + lr;
 #pragma unroll
@@ -871,13 +890,14 @@ __global__ __launch_bounds__(256) void bwd16_rows_kernel(BwdParams p, Ws ws) {
   }
 }
 
-template <int MAXT>
-__global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
-  __shared__ __attribute__((aligned(16))) __bf16 pt[kRows * kTp];  // P^T [16 keys][64 queries]
-  __shared__ __attribute__((aligned(16))) __bf16 dt[kRows * kTp];  // (dS * inv(query))^T
-  __shared__ float red[4 * kRows];
+template <int NW, int MAXT>
+__global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws) {
+  constexpr int KT = 16 * NW, TP = KT + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 pt[kRows * TP];  // P^T [16 keys][KT queries]
+  __shared__ __attribute__((aligned(16))) __bf16 dt[kRows * TP];  // (dS * inv(query))^T
+  __shared__ float red[NW * kRows];
   __shared__ float rad[kRows];
-  constexpr int dp = 64 * MAXT + 8;
+  constexpr int dp = 16 * NW * MAXT + 8;
   __shared__ __attribute__((aligned(16))) __bf16 kzl[kRows * dp];  // the block's key rows
   const int D = (int)p.D;
   const int64_t C = p.C, cp = ws.cp;
@@ -908,10 +928,10 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   f32x4 acc1[MAXT], acc2[MAXT];
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Query tiles start at multiples of 64 so that the 64 rows each one reads from
-  // the transposed copies stay inside their cp (a multiple of 64) columns.
-  const int64_t qstart = p.causal ? (k0 / kTile) * kTile : 0;
-  for (int64_t qt = qstart; qt < C; qt += kTile) {
+  // Query tiles start at multiples of KT so that the KT rows each one reads from
+  // the transposed copies stay inside their cp (a multiple of KT) columns.
+  const int64_t qstart = p.causal ? (k0 / KT) * KT : 0;
+  for (int64_t qt = qstart; qt < C; qt += KT) {
     const int64_t q = qt + 16 * w + lr;
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
@@ -929,12 +949,12 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
         pv = s4[i] * kinv[i] * q_inv * vv;
         dsv = (d4[i] + dd) * vv * q_inv;
       }
-      pt[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)pv;
-      dt[(4 * lg + i) * kTp + 16 * w + lr] = (__bf16)dsv;
+      pt[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)pv;
+      dt[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)dsv;
     }
     __syncthreads();
-    rows_acc16<MAXT>(acc1, pt, dntb, qt, D, cp, w, lr, lg);
-    rows_acc16<MAXT>(acc2, dt, ztb, qt, D, cp, w, lr, lg);
+    rows_acc16<NW, MAXT>(acc1, pt, dntb, qt, D, cp, w, lr, lg);
+    rows_acc16<NW, MAXT>(acc2, dt, ztb, qt, D, cp, w, lr, lg);
     __syncthreads();
   }
 
@@ -942,7 +962,7 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   float rp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
+    const int tile_i = w + NW * t;
     if (tile_i >= ntiles) break;
     const int col = 16 * tile_i + lr;
 #pragma unroll
@@ -967,7 +987,7 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
     float r = 0.f;
     if (row_valid(p.valid, b, C, k)) {
       const float n = ws.nrm[b * C + k];
-      if (n >= neps) r = (red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / n;
+      if (n >= neps) r = (sum_waves<NW>(red, i)) / n;
     }
     rad[i] = r;
   }
@@ -975,7 +995,7 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   __bf16* dzb = (__bf16*)p.dz + b * C * D;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
+    const int tile_i = w + NW * t;
     if (tile_i >= ntiles) break;
     const int col = 16 * tile_i + lr;
 #pragma unroll
@@ -992,7 +1012,7 @@ __global__ __launch_bounds__(256) void bwd16_cols_kernel(BwdParams p, Ws ws) {
   }
 }
 
-template <int MAXT>
+template <int NW, int MAXT>
 hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
   Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, true);
   const int64_t rows = p.B * p.C;
@@ -1000,8 +1020,8 @@ hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL(bwd16_transpose_kernel, dim3((unsigned)(ws.cp / 64), (unsigned)cdiv(p.D, 64), (unsigned)p.B),
                      dim3(256), 0, s, p, ws);
   const dim3 grid((unsigned)(cdiv(p.C, kRows) * p.B));  // 1-D, mapped by tile_of_block
-  hipLaunchKernelGGL((bwd16_rows_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
-  hipLaunchKernelGGL((bwd16_cols_kernel<MAXT>), grid, dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd16_rows_kernel<NW, MAXT>), grid, dim3(64 * NW), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd16_cols_kernel<NW, MAXT>), grid, dim3(64 * NW), 0, s, p, ws);
   if (p.dv || p.dbias) {
     const int64_t n = p.dv ? p.C * p.C : p.D;
     const int64_t blocks = cdiv(n, 256) < 1024 ? cdiv(n, 256) : 1024;
@@ -1035,12 +1055,13 @@ hipError_t launch_bwd_d(const BwdParams& p, hipStream_t s) {
   return launch_bwd_t<T, 16>(p, s);
 }
 
+// 8 waves per workgroup: each holds 16-column tiles of up to 8 x 16 features per
+// accumulator, so two waves share a SIMD and cover each other's operand loads.
 hipError_t launch_bwd16(const BwdParams& p, hipStream_t s) {
   const int64_t tiles = cdiv(p.D, 16);
-  if (tiles <= 8) return launch_bwd16_t<2>(p, s);
-  if (tiles <= 16) return launch_bwd16_t<4>(p, s);
-  if (tiles <= 32) return launch_bwd16_t<8>(p, s);
-  return launch_bwd16_t<16>(p, s);
+  if (tiles <= 16) return launch_bwd16_t<8, 2>(p, s);
+  if (tiles <= 32) return launch_bwd16_t<8, 4>(p, s);
+  return launch_bwd16_t<8, 8>(p, s);
 }
 
 }  // namespace

@@ -103,8 +103,8 @@ def test_backward_workspace_layout():
     full = _bwd_args(v=1 << 41, dv=1 << 44, bias=(1 << 41) + (1 << 30), dbias=1 << 45)
     assert lib.avey_bwd_workspace_bytes(ctypes.byref(full)) == plain + 4 * (up(c * c) + up(d))
     # bf16 rows of a multiple of 8 features (16-byte aligned z_tr): the bf16 path keeps
-    # z^T and dnum^T ([D][C rounded up to 64] bf16) and dnum in bf16 instead of fp32.
-    d8, cp = 40, 64
+    # z^T and dnum^T ([D][C rounded up to 128] bf16) and dnum in bf16 instead of fp32.
+    d8, cp = 40, 128
     fast = lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args(features=d8)))
     assert fast == 4 * (2 * up(b * c) + up(b * c * d8) + 2 * up(b * d8 * cp // 2) + up(b * c * d8 // 2))
     assert lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args(features=d8, dtype=1))) == \
