@@ -197,3 +197,40 @@ def test_autograd_only_requested_gradients():
     out.backward(c['dout'])
     want = _oracle_grads(c, eps=1e-6, causal=True, normalize=False, act='identity')
     _check([z.grad, None, None, None], [want[0], None, None, None], torch.float32, 'z only')
+
+
+def test_backward_is_deterministic_except_atomic_sums():
+    # dz_tr and dz_tl come from fixed-order sums; dv and dbias from float atomics.
+    c = _case(4, 130, 64, torch.bfloat16, seed=31, normalize=False, valid=True, nan_pad=False)
+    kw = dict(eps=1e-6, causal=True, normalize=False, act='gelu')
+    a = _hip_grads(c, **kw)
+    b = _hip_grads(c, **kw)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[2], b[2])
+    torch.testing.assert_close(a[1], b[1], rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(a[3], b[3], rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_backward_hip_graph_replays_match_eager(dtype):
+    """avey_bwd issues no memset (accumulators are cleared by a kernel), so it can be
+    captured; every replay, with eager work between them, matches the eager call."""
+    c = _case(2, 96, 64, dtype, seed=41, normalize=False, valid=True, nan_pad=False)
+    kw = dict(eps=1e-6, causal=True, normalize=False, act='silu')
+    eager = [t.clone() for t in _hip_grads(c, **kw)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _hip_grads(c, **kw)  # warm-up on the capture stream (allocator pools)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = _hip_grads(c, **kw)
+    for rep in range(3):
+        junk = torch.randn(1 << 20, device=DEV) * rep  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        del junk
+        assert torch.equal(static[0], eager[0]) and torch.equal(static[2], eager[2]), f'replay {rep}'
+        torch.testing.assert_close(static[1], eager[1], rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(static[3], eager[3], rtol=1e-2, atol=1e-2)
