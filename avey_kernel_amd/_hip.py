@@ -113,14 +113,30 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def readable_in_place(t):
+    """Whether the library can read a [B, C, D] operand at its own strides: the
+    features contiguous and the rows of a batch item apart by at least D elements
+    (a broadcast row stride of 0, or rows that overlap, need a contiguous copy; the
+    C ABI reads a row stride of 0 as "contiguous"). Dimensions of size 1 have no
+    meaningful stride and are not checked."""
+    batch, context, features = t.shape
+    if t.is_contiguous():
+        return True
+    return (features == 1 or t.stride(2) == 1) and (context == 1 or t.stride(1) >= features) \
+        and (batch == 1 or t.stride(0) >= 0)
+
+
 def row_strides(t):
-    """(row stride, batch stride) in elements of a [B, C, D] operand whose features
-    are contiguous; (0, 0) for a contiguous tensor or None."""
+    """(row stride, batch stride) in elements of a [B, C, D] operand the library
+    reads in place; (0, 0) for a contiguous tensor or None. Size-1 dimensions get
+    the strides of a contiguous layout."""
     if t is None or t.is_contiguous():
         return 0, 0
-    if t.stride(2) != 1:
-        raise ValueError('z_tr / z_tl need a contiguous last dimension')
-    return t.stride(1), t.stride(0)
+    if not readable_in_place(t):
+        raise ValueError('z_tr / z_tl need contiguous features and rows at least D elements apart')
+    batch, context, features = t.shape
+    row = t.stride(1) if context > 1 else features
+    return row, (t.stride(0) if batch > 1 else context * row)
 
 
 def make_args(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, activation):
@@ -190,9 +206,9 @@ def contextualize(z_tr: torch.Tensor, v: Optional[torch.Tensor], z_tl: Optional[
     """out = z_tl * act(mix(z_tr) / den + bias), fused on the GPU. z_tr and z_tl may be
     strided views with a contiguous last dimension; out is contiguous."""
     # Callers such as Inductor hand over whatever layouts their graph chose: views
-    # with contiguous features go through as they are, anything else is made so.
-    z_tr = z_tr if z_tr.stride(-1) == 1 else z_tr.contiguous()
-    if z_tl is not None and z_tl.stride(-1) != 1:
+    # the library reads in place go through as they are, anything else is made so.
+    z_tr = z_tr if readable_in_place(z_tr) else z_tr.contiguous()
+    if z_tl is not None and not readable_in_place(z_tl):
         z_tl = z_tl.contiguous()
     v, bias, valid = (None if t is None else t.contiguous() for t in (v, bias, valid))
     out = torch.empty_like(z_tr, memory_format=torch.contiguous_format)

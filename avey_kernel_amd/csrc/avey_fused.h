@@ -234,10 +234,12 @@ struct Geo {
   static constexpr int P = CPRP / 4;
   static constexpr int RPP = 16;
   static constexpr int SX = kWaves * 2 * QB * 64 * 16;
+  // One plane of P (16-bit MFMA operands, a sink row for idle units); the
+  // normalised variants keep a second plane for the low part of P.
   static constexpr int PX = (QB + 1) * 64 * 16;
   // The query rows of the prologue take ring slot R-1 and, for BM = 64, this
-  // region too, which later holds the partial similarities and P.
-  static constexpr int OVF = (BM > 32 && TILE > SX + PX) ? TILE : SX + PX;
+  // region too, which later holds the partial similarities and both planes of P.
+  static constexpr int OVF = (BM > 32 && TILE > SX + 2 * PX) ? TILE : SX + 2 * PX;
   static constexpr int SMALL = 4 * (kWaves * kBN + kBN + kWaves * BM + BM + (QB + 1) * 2 * 4 * 16 + BM);
   static constexpr int kLdsMax = 160 * 1024;
   // Ring depth: three slots where they fit, else two.
@@ -309,7 +311,12 @@ __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0x
 // chunk wholly in or out). STRIDED: z_tr / z_tl rows and batch items are apart by
 // the strides in FwdParams; otherwise contiguous (a separate instantiation: the
 // runtime strides cost registers, and the 64-row variants then spill more).
-template <typename T16, int BM, int NK, bool FULL, bool STRIDED>
+// HILO (the normalised, Avey-B calls): the mixing product takes P as two 16-bit
+// parts, P_hi = rnd(P) and P_lo = rnd(P - P_hi), in two MFMAs into the same fp32
+// accumulator. P then enters the numerator to about 2^-17 (bf16) of itself, as
+// the denominator's fp32 sum does; with P_hi alone, rows whose signed sum cancels
+// amplify the 2^-9 rounding of each term past the bf16 bound.
+template <typename T16, int BM, int NK, bool FULL, bool STRIDED, bool HILO>
 __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(FwdParams p) {
   typedef Geo<BM, NK> Gm;
   constexpr bool WS = Gm::WS, QS = Gm::QS;
@@ -331,6 +338,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   static_assert(sizeof(SmallLds<BM>) <= Gm::SMALL, "small LDS arrays");
   f32x4(*const sx)[2][QB][64] = reinterpret_cast<f32x4(*)[2][QB][64]>(ovf);           // [wave][kb][qb][lane]
   u32x4(*const px)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX);                // [qb (QB: sink)][lane]
+  u32x4(*const pxl)[64] = reinterpret_cast<u32x4(*)[64]>(ovf + Gm::SX + Gm::PX);      // P_lo, as px (HILO)
 
   // The wave index is read into a scalar register, so that LDS addresses built
   // from it (DMA destinations go through M0) stay scalar.
@@ -704,7 +712,14 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
         pv[i] = __uint_as_float(__float_as_uint(x) & keep);
         den[j] += pv[i];
       }
-      reinterpret_cast<u32x2*>(&px[pq[j]][lane])[kb] = u32x2{pack2<T16>(pv[0], pv[1]), pack2<T16>(pv[2], pv[3])};
+      const uint32_t h01 = pack2<T16>(pv[0], pv[1]), h23 = pack2<T16>(pv[2], pv[3]);
+      reinterpret_cast<u32x2*>(&px[pq[j]][lane])[kb] = u32x2{h01, h23};
+      if constexpr (HILO) {
+        // P - P_hi is exact in fp32 (P_hi holds P's leading bits); its rounding is P_lo.
+        const float l0 = pv[0] - Ops<T16>::to_f(h01 & 0xffffu), l1 = pv[1] - Ops<T16>::hi_f(h01);
+        const float l2 = pv[2] - Ops<T16>::to_f(h23 & 0xffffu), l3 = pv[3] - Ops<T16>::hi_f(h23);
+        reinterpret_cast<u32x2*>(&pxl[pq[j]][lane])[kb] = u32x2{pack2<T16>(l0, l1), pack2<T16>(l2, l3)};
+      }
     }
     load_v(t + 1 < nkt ? (t + 1) * kBN : C, vv);
   };
@@ -728,6 +743,16 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
         if (m % 2 == 0 && KA + m / 2 < KD && FETCH && (UNCOND || refill))
           fetch_key_share(tf, slot_base(fslot), KA + m / 2, kof, refill);
       }
+    if constexpr (HILO) {
+      // The low part of P, one query block at a time (its operand is live for one
+      // block only: the 64-row variants' registers are full).
+#pragma unroll
+      for (int qb = 0; qb < QBW; ++qb) {
+        const u32x4 pl = pxl[qb0 + qb][lane];
+#pragma unroll
+        for (int t2 = 0; t2 < NT; ++t2) oacc[t2][qb] = Ops<T16>::mfma32(ztr[t2], pl, oacc[t2][qb]);
+      }
+    }
     if (FETCH && (UNCOND || refill)) {
 #pragma unroll
       for (int j = KA + (NT * QBW + 1) / 2; j < KD; ++j) fetch_key_share(tf, slot_base(fslot), j, kof, refill);
@@ -1082,10 +1107,19 @@ hipError_t launch_fused_bm(const FwdParams& p, int nk, int64_t grid, hipStream_t
 
 template <typename T16, int BM, int NK, bool STRIDED>
 hipError_t launch_fused_one(const FwdParams& p, int64_t grid, hipStream_t s) {
-  if (p.D == 4 * 32 * NK)
-    fused_fwd_kernel<T16, BM, NK, true, STRIDED><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
-  else
-    fused_fwd_kernel<T16, BM, NK, false, STRIDED><<<dim3((unsigned)grid), dim3(Geo<BM, NK>::THREADS), 0, s>>>(p);
+  const dim3 g((unsigned)grid), t(Geo<BM, NK>::THREADS);
+  const bool full = p.D == 4 * 32 * NK;
+  if (p.normalize != 0) {
+    if (full)
+      fused_fwd_kernel<T16, BM, NK, true, STRIDED, true><<<g, t, 0, s>>>(p);
+    else
+      fused_fwd_kernel<T16, BM, NK, false, STRIDED, true><<<g, t, 0, s>>>(p);
+  } else {
+    if (full)
+      fused_fwd_kernel<T16, BM, NK, true, STRIDED, false><<<g, t, 0, s>>>(p);
+    else
+      fused_fwd_kernel<T16, BM, NK, false, STRIDED, false><<<g, t, 0, s>>>(p);
+  }
   return hipGetLastError();
 }
 

@@ -15,11 +15,13 @@ Backends (``backend=``):
   GPUs, fp64 or wider rows under autograd). The reference sends every
   gradient-requiring call to ``_reference`` (``ops.py:96-106``). On a gfx950 device a
   missing or broken ``libavey_hip.so`` raises instead of falling back.
-* ``'hip'``    the fused HIP kernel, or ``ValueError`` when it cannot run.
-* ``'triton'`` accepted for source compatibility: it names the reference's
-  fused GPU kernel, so it selects the fused HIP kernel here, with the same
-  ``ValueError`` when the fused path cannot run (``ops.py:101-103``).
+* ``'triton'`` raises ``ValueError`` with the reference's message, as the
+  reference does on every ROCm build (``ops.py:98-103``: its Triton path needs
+  ``torch.version.hip is None``), with or without gradients.
 * ``'torch'``  the eager PyTorch path (differentiable).
+* ``'hip'``    an extension of this build (not in the reference): the fused HIP
+  kernel, or ``ValueError`` when it cannot run. The validation message for an
+  unknown backend stays the reference's.
 
 ``output_tile`` and ``autotune`` are validated exactly as the reference does
 (``ops.py:30-33``) and are otherwise advisory: tiles come from the library's
@@ -45,7 +47,8 @@ def _validate(z_tr, v, z_tl, bias, valid, eps, norm_eps, activation, backend, ou
     if z_tr.dtype not in _FLOAT_DTYPES:
         raise ValueError('z_tr must be floating point')
     if backend not in _BACKENDS:
-        raise ValueError('backend must be auto, torch, triton, or hip')
+        # The reference's message ('hip' is this build's extension, accepted as well).
+        raise ValueError('backend must be auto, torch, or triton')
     # `type(...) is int` rejects bool and float tile widths, as the reference does.
     if type(output_tile) is not int or output_tile not in (32, 64, 128):
         raise ValueError('output_tile must be 32, 64, or 128')
@@ -129,8 +132,8 @@ def _fused_device(t):
 
 
 def _rows(t):
-    """t itself when its features are contiguous (any row / batch strides), else a copy."""
-    return t if t.stride(-1) == 1 else t.contiguous()
+    """t itself when the library can read it in place, else a contiguous copy."""
+    return t if _hip.readable_in_place(t) else t.contiguous()
 
 
 def _dispatch(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation, backend,
@@ -141,16 +144,22 @@ def _dispatch(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, acti
     # With gradients the fused forward runs when the fused backward (avey_bwd) covers
     # the inputs; otherwise autograd differentiates the eager path, which is what the
     # reference always does for gradients (ops.py:96-106).
+    if backend == 'triton':
+        # The reference's Triton path requires a CUDA (non-ROCm) PyTorch build
+        # (ops.py:98-103); on ROCm it always raises, and so does this build.
+        raise ValueError('Triton requires Triton installed, NVIDIA SM80+, and CUDA '
+                         'FP16/BF16/FP32 inference inputs; use backend="torch" for autograd')
     fused_ok = _fused_device(z_tr) and (not needs_grad or _hip.backward_supported(z_tr))
-    if backend in ('hip', 'triton') and not fused_ok:
+    if backend == 'hip' and not fused_ok:
         raise ValueError('the fused HIP kernel needs ROCm tensors on a gfx950 (MI355X) GPU; with '
                          'gradients also bf16 / fp16 / fp32 and at most 1024 features; use '
                          'backend="torch" for other inputs')
     if backend == 'torch' or not fused_ok:
         return _eager(z_tr, v, z_tl, bias, valid, eps, norm_eps, causal, normalize, activation)
     # The fused path, one launch. z_tr / z_tl go in as they are when their features
-    # are contiguous (strided views such as the halves of the enricher output: the
-    # library takes their row and batch strides), where ops.py:109-113 copies them;
+    # are contiguous and their rows do not overlap (strided views such as the halves
+    # of the enricher output: the library takes their row and batch strides), where
+    # ops.py:109-113 copies them; other layouts (broadcast or overlapping rows) and
     # the other operands are made contiguous as there.
     return torch.ops.avey_kernels.contextualize(
         _rows(z_tr), v.contiguous() if v is not None else None,

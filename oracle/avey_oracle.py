@@ -23,7 +23,7 @@ Pinning (each check lives in ``tests/test_oracle.py``):
   points, and ``torch.nn.functional`` on random points.
 * ``contextualize``: the reference's hand-computed known answers
   (``tests/test_contextualizer.py:13-39``, ``tests/test_profiling.py:46-61``,
-  ``tests/test_triton.py:251-258``), transcribed into
+  ``tests/test_triton.py:162-169``), transcribed into
   ``tests/golden/kats.json``; the independent C restatement
   ``oracle/avey_oracle.c`` (a per-query streaming loop, no N x N matrix) on
   random inputs with every flag combination; invariants (causal output rows
@@ -35,6 +35,10 @@ Pinning (each check lives in ``tests/test_oracle.py``):
 * ``key_tile_count``: the reference's closed-form table
   (``tests/test_causal_skip.py:52-60``) and a brute-force count of tiles
   holding at least one allowed (query, key) pair.
+* ``row_condition`` (a diagnostic printed next to Avey-B results; no test
+  bound depends on it except the fp32 subset of rows held to 1e-5): closed
+  forms on rows with similarities +-1 / 0 (cancelling sums, eps inside the
+  absolute value, padded keys dropped) and an explicit loop over keys.
 """
 
 import math
@@ -158,8 +162,9 @@ def key_tile_count(query_tile, c, bm, bn, causal, skip=True):
 def row_condition(z_tr, valid=None, *, eps=1e-6, norm_eps=1e-12):
     """Per-row conditioning of the Avey-B denominator, sum|S_ij| / |sum S_ij + eps|.
 
-    Used only to report how much a row amplifies rounding (no reference
-    counterpart; derived from ops.py:79-80).
+    Reports how much a row amplifies rounding (no reference counterpart;
+    derived from ops.py:79-80). S is symmetric, so summing over keys or over
+    queries gives the same values.
     """
     z = np.array(z_tr, dtype=np.float64, copy=True)
     if valid is not None:

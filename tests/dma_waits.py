@@ -66,7 +66,7 @@ def ring(bm, nk):
     tile = 4 * 32 * cprp * 16
     qb = bm // 16
     sx, px = 4 * 2 * qb * 64 * 16, (qb + 1) * 64 * 16
-    ovf = tile if (bm > 32 and tile > sx + px) else sx + px
+    ovf = tile if (bm > 32 and tile > sx + 2 * px) else sx + 2 * px  # two planes of P
     small = 4 * (4 * 32 + 32 + 4 * bm + bm + (qb + 1) * 2 * 4 * 16 + bm)
     r = 3 if 3 * tile + ovf + small <= 160 * 1024 else 2
     share = 2 if query_split(bm, nk) else 1

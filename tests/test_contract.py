@@ -162,3 +162,84 @@ def test_make_fx_records_exactly_one_fused_call():
     graph = make_fx(fn, tracing_mode='fake')(torch.empty(2, 35, 37), torch.empty(2, 35, 37))
     calls = [n for n in graph.graph.nodes if 'contextualize' in str(n.target)]
     assert len(calls) == 1
+
+
+# The drop-in package: a reference caller's imports (`from avey_kernels import avey,
+# avey_b`, avey_kernels/__init__.py:3-5; `avey_kernels.ops.avey`, ops.py:117-147)
+# resolve to this build and give the reference's known answers.
+@pytest.mark.parametrize('case', KATS['cases'], ids=[c['name'] for c in KATS['cases']])
+def test_drop_in_package_known_answers(case):
+    import avey_kernels
+    import avey_kernels.ops as ak_ops
+    assert avey_kernels.avey is ak_ops.avey and avey_kernels.avey_b is ak_ops.avey_b
+    assert avey_kernels.__all__ == ['avey', 'avey_b']
+    dt = torch.float64 if case['dtype'] == 'float64' else torch.float32
+    z = torch.tensor(case['z_tr'], dtype=dt)
+    kw = dict(case['kwargs'])
+    for key in ('z_tl', 'bias'):
+        if key in case:
+            kw[key] = torch.tensor(case[key], dtype=dt)
+    if 'valid' in case:
+        kw['valid'] = torch.tensor(case['valid'])
+    if case['op'] == 'avey':
+        out = ak_ops.avey(z, torch.tensor(case['v'], dtype=dt), **kw)
+    else:
+        out = ak_ops.avey_b(z, **kw)
+    want = case.get('expected')
+    if want is None:
+        torch.testing.assert_close(out[0, 0], torch.tensor(case['expected_row0'], dtype=dt))
+    else:
+        torch.testing.assert_close(out, torch.tensor(want, dtype=dt), rtol=case['rtol'], atol=case['atol'])
+    # The eager path under the reference's own name.
+    args = (z, torch.tensor(case['v'], dtype=dt) if case['op'] == 'avey' else None, kw.get('z_tl'), kw.get('bias'),
+            kw.get('valid'))
+    normalize = case['op'] == 'avey_b'
+    ref = ak_ops._reference(*args, kw.get('eps', 1e-6) if normalize else 1e-6, 1e-12,
+                            kw.get('causal', not normalize) and not normalize, normalize,
+                            kw.get('activation', 'identity'))
+    torch.testing.assert_close(ref, out)
+
+
+def test_triton_backend_raises_like_the_reference_on_rocm():
+    # ops.py:98-103: the reference's Triton path needs a CUDA (non-ROCm) build, so on
+    # ROCm backend='triton' raises ValueError, with and without gradients
+    # (tests/test_triton.py:217-224).
+    import avey_kernels
+    z = torch.rand(2, 5, 4)
+    for requires_grad in (False, True):
+        zz = z.clone().requires_grad_(requires_grad)
+        with pytest.raises(ValueError, match='Triton requires'):
+            avey_kernels.avey_b(zz, backend='triton')
+        with pytest.raises(ValueError, match='Triton requires'):
+            avey_kernels.avey(zz, torch.rand(5, 5), backend='triton')
+
+
+def test_unknown_backend_message_is_the_references():
+    with pytest.raises(ValueError, match=r'^backend must be auto, torch, or triton$'):
+        avey_b(torch.ones(1, 3, 2), backend='cuda')
+
+
+def test_layouts_read_in_place_or_copied():
+    # The C ABI reads a row stride of 0 as "contiguous", so broadcast rows (stride 0)
+    # and overlapping rows (0 < stride < D) must reach it as contiguous copies;
+    # views with contiguous features and rows >= D apart go in place.
+    base = torch.randn(2, 1, 64)
+    expanded = base.expand(2, 8, 64)
+    assert expanded.stride(1) == 0 and not _hip.readable_in_place(expanded)
+    flat = torch.randn(2, 200)
+    overlapping = flat.unfold(1, 64, 16)  # [2, 9, 64], rows 16 apart
+    assert overlapping.stride() == (200, 16, 1) and not _hip.readable_in_place(overlapping)
+    halves = torch.randn(3, 5, 128)[..., 64:]
+    assert _hip.readable_in_place(halves) and _hip.row_strides(halves) == (128, 640)
+    batch_bcast = torch.randn(1, 5, 64).expand(4, 5, 64)
+    assert _hip.readable_in_place(batch_bcast) and _hip.row_strides(batch_bcast) == (64, 0)
+    one_row = torch.randn(4, 3, 64)[:, 1:2]  # context 1: its row stride is meaningless
+    assert _hip.row_strides(one_row) == (64, 192)
+    for bad in (expanded, overlapping):
+        with pytest.raises(ValueError):
+            _hip.row_strides(bad)
+    from avey_kernel_amd import ops
+    for t in (expanded, overlapping, torch.randn(2, 64, 8).transpose(1, 2)):
+        r = ops._rows(t)
+        assert r.is_contiguous() and torch.equal(r, t)
+    assert ops._rows(halves) is halves

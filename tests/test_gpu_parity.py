@@ -52,11 +52,19 @@ def _report(out, want):
     return float(diff.max()), float(row_err.max())
 
 
+# fp32 Avey-B: the reference's own bound for its fp32 kernel against its fp32 eager
+# path on signed random inputs with eps = 0.25 (tests/test_triton.py:155-160). Any
+# fp32 arithmetic, the reference's included, misses 1e-5 on rows whose signed sum
+# cancels (row condition ~3e3 at C = 67, D = 65 here: 2e-4); rows with condition
+# below 10 must still meet 1e-5.
+FP32_NORMALIZED_TOL = 3e-4
+
+
 def _assert_close(out, want, dtype, label='', cond=None):
-    """allclose at the dtype's tolerance; with ``cond`` (per-row Avey-B condition
-    numbers) the tolerance of each row grows with its conditioning, the way a
-    sum that cancels amplifies rounding (the reference relaxes to 3e-4 for the
-    same reason, tests/test_triton.py:243-249)."""
+    """Flat allclose(rtol = atol = the dtype's tolerance) against the fp64 oracle.
+
+    ``cond`` (per-row Avey-B condition numbers, sum|S| / |sum S + eps|) is only
+    printed, except for fp32 (see FP32_NORMALIZED_TOL)."""
     out = _np(out)
     tol = TOL[dtype]
     # Values beyond the output type's range round to +-inf in the reference's
@@ -70,13 +78,22 @@ def _assert_close(out, want, dtype, label='', cond=None):
         want = np.where(over, 0.0, want)
     max_abs, row = _report(out, want)
     if cond is not None:
-        scale = (1.0 + cond)[..., None]
-        bad = np.abs(out - want) > tol * scale * (1.0 + np.abs(want))
-        assert not bad.any(), f'{label} {int(bad.sum())} elements beyond tol*(1+cond); max_abs={max_abs:.3e}'
-        return max_abs, row
+        print(f'[{label}] row condition: max {float(cond.max()):.3e}, rows > 10: {int((cond > 10).sum())}/{cond.size}; '
+              f'max_abs={max_abs:.3e}', flush=True)
+        if dtype == torch.float32:
+            good = cond < 10
+            np.testing.assert_allclose(out[good], want[good], rtol=tol, atol=tol, err_msg=f'{label} cond<10')
+            tol = FP32_NORMALIZED_TOL
     np.testing.assert_allclose(out, want, rtol=tol, atol=tol, err_msg=f'{label} max_abs={max_abs:.3e} row={row:.3e}')
     if dtype == torch.bfloat16:
-        assert row <= 1e-2, f'{label} row-normwise error {row:.3e}'
+        # The row-normwise bound (the build's own, on top of the elementwise one) holds
+        # on rows whose conditioning lets fp32 arithmetic meet it: a row with condition
+        # k has a relative error near 6e-8 k in any fp32 computation, the reference's
+        # included (1.3e-2 at k = 1.3e6 was seen), so rows with k >= 1e3 are reported.
+        rows = slice(None) if cond is None else cond < 1e3
+        if out[rows].size:
+            _, row_ok = _report(out[rows], want[rows])
+            assert row_ok <= 1e-2, f'{label} row-normwise error {row_ok:.3e}'
     return max_abs, row
 
 
@@ -169,12 +186,9 @@ def test_benchmark_configs_full_size(tag):
                    eps=1e-6, causal=cfg.causal, normalize=normalize, act='identity', acc=acc)
     cond = None
     if normalize:
+        # Diagnostic only: every element meets the flat bound whatever its row's conditioning.
         cond = orc.row_condition(_np(inp['z_tr']), None if inp['valid'] is None else inp['valid'].cpu().numpy())
-        print(f'[{cfg.name}] Avey-B row condition: median {np.median(cond):.2f} max {cond.max():.3e} '
-              f'rows>10: {int((cond > 10).sum())}/{cond.size}', flush=True)
-        # Well-conditioned rows must meet the plain bound as well.
-        good = cond < 4
-        _assert_close(out.cpu()[torch.from_numpy(good)], want[good], cfg.dtype, cfg.name + ' cond<4')
+        print(f'[{cfg.name}] Avey-B row condition: median {np.median(cond):.2f}', flush=True)
     max_abs, row = _assert_close(out, want, cfg.dtype, cfg.name, cond)
     print(f'[{cfg.name}] max_abs={max_abs:.3e} row_normwise={row:.3e}', flush=True)
 
@@ -482,3 +496,47 @@ def test_results_do_not_depend_on_stale_lds(bm, d, dtype):
         torch.cuda.synchronize()
         assert not torch.isnan(warm).any(), (bm, d, label)
         assert torch.equal(cold, warm), (bm, d, label, (cold.float() - warm.float()).abs().nan_to_num(1e9).max())
+
+
+def test_triton_backend_raises_on_rocm_gpu_tensors():
+    # As the reference on any ROCm build (ops.py:98-103; tests/test_triton.py:217-224).
+    import avey_kernels
+    z = torch.rand(2, 37, 35, device=DEV).transpose(1, 2)
+    with pytest.raises(ValueError):
+        avey_kernels.avey_b(z, backend='triton')
+    z.requires_grad_()
+    with pytest.raises(ValueError):
+        avey_kernels.avey_b(z, backend='triton')
+    # The default backend takes the fused path and matches the eager one.
+    zb = torch.rand(2, 35, 64, device=DEV, dtype=torch.bfloat16)
+    out = avey_kernels.avey_b(zb)
+    want = _oracle(zb, None, None, None, None, eps=1e-6, causal=False, normalize=True, act='identity')
+    _assert_close(out, want, torch.bfloat16, 'avey_kernels.avey_b')
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'fp32'])
+def test_broadcast_and_overlapping_rows_match_oracle(dtype):
+    # z_tr / z_tl views whose rows repeat (expand: row stride 0) or overlap (unfold:
+    # row stride < D) are copied before the library sees them; the library itself
+    # would read a row stride of 0 as contiguous. Positive inputs keep the Avey-B row
+    # sums away from cancellation (overlapping rows are strongly correlated), as the
+    # reference's own low-precision tests do (tests/test_triton.py:193-195).
+    g = torch.Generator().manual_seed(23)
+    d, c = 64, 40
+    base = torch.rand(3, 1, d, generator=g).to(DEV, dtype)
+    z_rep = base.expand(3, c, d)                                   # every row the same
+    flat = torch.rand(3, c * 16 + d, generator=g).to(DEV, dtype)
+    z_ovl = flat.unfold(1, d, 16)[:, :c]                           # rows 16 apart, overlapping
+    gate = torch.randn(3, 1, d, generator=g).to(DEV, dtype).expand(3, c, d)
+    v = ((torch.rand(c, c, generator=g) * 2 - 1) / c ** 0.5).to(DEV, dtype)
+    for z in (z_rep, z_ovl):
+        assert not _hip.readable_in_place(z)
+        for normalize in (False, True):
+            if normalize:
+                out = avey_b(z, z_tl=gate, eps=0.25, backend='hip')
+            else:
+                out = avey(z, v, z_tl=gate, backend='hip')
+            want = _oracle(z, None if normalize else v, gate, None, None, eps=0.25 if normalize else 1e-6,
+                           causal=not normalize, normalize=normalize, act='identity')
+            cond = orc.row_condition(_np(z), eps=0.25) if normalize else None
+            _assert_close(out, want, dtype, f'stride {z.stride()} normalize={normalize}', cond)

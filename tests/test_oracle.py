@@ -247,3 +247,36 @@ def test_planted_mistakes_are_caught_by_known_answers(variant):
         except AssertionError:
             caught = True
     assert caught, f'{variant.__name__} passes every known answer'
+
+
+# row_condition: sum_j |S_ij| / |sum_j S_ij + eps| (the Avey-B denominator of
+# ops.py:79-80). Closed forms on rows whose cosine similarities are +-1 or 0, so
+# that a dropped eps (division by zero), eps added outside the absolute value, an
+# absolute value inside the signed sum, or padded keys left in, each fail one case.
+@pytest.mark.parametrize('z,valid,eps,want', [
+    # S = [[1, -1], [-1, 1]]: both signed sums cancel to 0, so |0 + 0.5| sets it.
+    ([[1., 0.], [-2., 0.]], None, 0.5, [4.0, 4.0]),
+    # S = [[1,1,-1],[1,1,-1],[-1,-1,1]]: sums 1, 1, -1; |-1 + 0.25| = 0.75 for the last row.
+    ([[1., 0.], [3., 0.], [-1., 0.]], None, 0.25, [3 / 1.25, 3 / 1.25, 3 / 0.75]),
+    # Orthogonal rows: S = I.
+    ([[3., 4.], [4., -3.]], None, 1e-6, [1 / (1 + 1e-6)] * 2),
+    # A padded key (row 2) is dropped from both sums; the padded row itself has S = 0.
+    ([[1., 0.], [-2., 0.], [7., 1.]], [True, True, False], 0.5, [4.0, 4.0, 0.0]),
+])
+def test_row_condition_closed_forms(z, valid, eps, want):
+    z = np.asarray([z])
+    valid = None if valid is None else np.asarray([valid])
+    np.testing.assert_allclose(orc.row_condition(z, valid, eps=eps)[0], want, rtol=1e-12)
+
+
+def test_row_condition_matches_a_loop_over_keys():
+    rng = np.random.default_rng(11)
+    z = rng.standard_normal((2, 9, 5))
+    valid = rng.random((2, 9)) > 0.3
+    got = orc.row_condition(z, valid, eps=0.1)
+    for b in range(2):
+        for i in range(9):
+            zi = z[b, i] if valid[b, i] else np.zeros(5)
+            s = [0.0 if not (valid[b, i] and valid[b, j]) else
+                 float(zi @ z[b, j]) / (np.linalg.norm(zi) * np.linalg.norm(z[b, j])) for j in range(9)]
+            assert abs(got[b, i] - sum(map(abs, s)) / abs(sum(s) + 0.1)) < 1e-12 * (1 + got[b, i])
