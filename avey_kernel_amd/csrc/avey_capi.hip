@@ -1,5 +1,6 @@
 // C ABI of libavey_hip.so: argument checks, the static tile table, dispatch.
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <atomic>
@@ -83,6 +84,19 @@ int slice_steps(int64_t D) {
   return 0;
 }
 
+// Profiling override of the table's row-block height (environment variable
+// AVEY_PLAN_BM = 16, 32 or 64), read once. It exists to measure the alternatives
+// the table rejects with the same counters as its choices; a height that is not
+// compiled for the row width (32 / 64 rows with more than 768 features) is ignored.
+int forced_bm() {
+  static const int bm = [] {
+    const char* s = getenv("AVEY_PLAN_BM");
+    const int v = s ? atoi(s) : 0;
+    return (v == 16 || v == 32 || v == 64) ? v : 0;
+  }();
+  return bm;
+}
+
 bool device_ok(int dev) {
   if (dev < 0 || dev >= kMaxDevices) return false;
   int st = g_device_ok[dev].load(std::memory_order_relaxed);
@@ -131,6 +145,7 @@ Plan make_plan(const avey_fwd_args& a) {
     // state does not fit 256 registers) and was 1.23x slower on B4 N2048 causal.
     int bm = nk <= 6 ? 64 : 16;
     while (bm > 16 && cdiv(a.context, bm) * a.batch < 256) bm /= 2;
+    if (forced_bm() != 0 && (forced_bm() == 16 || nk <= 6)) bm = forced_bm();
     pl.bm = bm;
     pl.threads = fused_threads(bm, nk);
     const int64_t nqt = cdiv(a.context, bm);

@@ -104,6 +104,12 @@ def useful_flops(cfg, valid=None):
     return 4 * cfg.features * allowed_pairs(cfg, valid)
 
 
+def dense_flops(cfg):
+    """Dense-equivalent flops: every (query, key) pair, as the eager path computes them
+    (two dense B x C x C x D products, ops.py:69,78). Reported only as such."""
+    return 4 * cfg.features * cfg.batch * cfg.context * cfg.context
+
+
 def compulsory_bytes(cfg, with_v=None):
     es = torch.finfo(cfg.dtype).bits // 8
     with_v = (cfg.op == 'avey') if with_v is None else with_v

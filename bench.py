@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark the fused Avey / Avey-B forward contextualizer on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config C2] [--all-configs]
+    python bench.py [--steps K] [--warmup W] [--config C2] [--headline-only]
 
 A step is one call of the hot path (``avey`` / ``avey_b``) on one batch of the
 configuration's synthetic, seeded inputs, already resident in HBM. The timed
@@ -14,9 +14,16 @@ F = 4 * D * (allowed query-key pairs); compulsory bytes M = z_tr + z_tl + out
 (+ V, bias, valid). The headline C2 config (AI = 85 flop/B) sits below the
 MI355X ridge (315 flop/B), so its roofline is HBM.
 
-The CPU baseline times the numpy oracle (oracle/avey_oracle.py, fp32 like the
-reference's eager path) on the host cores, on the full config for about
-``--cpu-seconds`` of work; it is a reported baseline only.
+Besides the warm (back-to-back, MALL-resident) figure, every configuration is
+also timed cold: each of ``--cold-calls`` calls follows a 512 MiB write that
+evicts the 256 MB MALL and the L2s. A single call's event span carries launch
+overhead, so the cold kernel time is the warm graph time plus the difference
+between cold and warm single-call spans measured the same way.
+
+The CPU baseline times the torch-eager restatement of the reference's path
+(oracle/avey_torch_ref.py, what the reference runs on ROCm, fp32 accumulation,
+dense N x N) under ``torch.inference_mode()`` on the host cores, at the default
+thread count and at one thread; it is a reported baseline only.
 """
 
 import argparse
@@ -31,6 +38,7 @@ METRIC = 'contextualizer fwd µs/call + TFLOP/s (MFMA util %), bf16 B16×N256×D
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_HBM_GBPS = 8000.0
 RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBPS * 1e9)
+SPANS = {}  # config tag -> (cold, warm) median single-call event spans in us
 
 
 def parse_args():
@@ -39,13 +47,14 @@ def parse_args():
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=20)
     ap.add_argument('--config', default='C2')
-    ap.add_argument('--cpu-seconds', type=float, default=10.0)
+    ap.add_argument('--cpu-seconds', type=float, default=6.0,
+                    help='bound on the CPU baseline time per thread setting (at least 10 calls are timed)')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
-    ap.add_argument('--cold-calls', type=int, default=0,
-                    help='also time this many calls with the MALL flushed before each (off by default so that '
-                         'every traced dispatch of the default run is a warm one)')
-    ap.add_argument('--all-configs', action='store_true',
-                    help='also measure every configuration (table on stderr, --report JSON)')
+    ap.add_argument('--cold-calls', type=int, default=20,
+                    help='calls timed with the MALL and L2s flushed before each (0: skip)')
+    ap.add_argument('--headline-only', action='store_true',
+                    help='skip the per-configuration table (C1-C5) in extra.configs')
+    ap.add_argument('--all-configs', action='store_true', help=argparse.SUPPRESS)  # the table is on by default
     ap.add_argument('--report', default=None, help='write all measurements to this JSON file')
     ap.add_argument('--dispatches', type=int, default=0,
                     help='profiling run: launch the config this many times (eager, no timing, no JSON) '
@@ -102,10 +111,11 @@ def measure_eager(torch, fn, steps):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def measure_cold(torch, fn, calls):
-    """Per-call kernel span with the 256 MB MALL flushed by a 512 MiB write before each call."""
-    scratch = torch.empty(512 << 20, dtype=torch.uint8, device='cuda')
-    spans = []
+def measure_single_calls(torch, fn, calls, flush):
+    """Median event span of single calls, each after a 512 MiB write (flush=True,
+    which evicts the 256 MB MALL and every L2) or after a small write on the
+    same stream (flush=False: a 4 KiB write, the inputs stay resident)."""
+    scratch = torch.empty((512 << 20) if flush else 4096, dtype=torch.uint8, device='cuda')
     evs = []
     for i in range(calls):
         scratch.fill_(i & 0xFF)
@@ -115,45 +125,54 @@ def measure_cold(torch, fn, calls):
         b.record()
         evs.append((a, b))
     torch.cuda.synchronize()
-    for a, b in evs:
-        spans.append(a.elapsed_time(b))
     del scratch
-    return statistics.median(spans)
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
 
 
-def cpu_baseline(cfg, inputs_cpu, seconds):
-    """Time the numpy oracle (fp32, the reference's eager arithmetic) on the host."""
-    import numpy as np
-    from oracle import avey_oracle as orc
+def host_cpu_model():
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([d.get('num_threads', 1) for d in threadpool_info()] or [1])
+        import subprocess
+        out = subprocess.run(['lscpu'], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith('Model name:'):
+                return line.split(':', 1)[1].strip()
     except Exception:  # pragma: no cover - reporting only
-        cores = os.cpu_count() or 1
-    z = inputs_cpu['z_tr'].float().numpy()
-    gate = inputs_cpu['z_tl'].float().numpy()
-    bias = inputs_cpu['bias'].float().numpy()
-    v = inputs_cpu['v'].float().numpy()
-    valid = None if inputs_cpu['valid'] is None else inputs_cpu['valid'].numpy()
+        pass
+    return 'unknown'
+
+
+def cpu_baseline(torch, cfg, inputs_cpu, seconds, threads):
+    """Median seconds per call of the torch-eager restatement of the reference's path
+    (oracle/avey_torch_ref.py) on the CPU at `threads` threads: 2 warm-up calls, then
+    at least 10 timed calls and at least one second, bounded by `seconds`."""
+    from oracle import avey_torch_ref as tref
     normalize = cfg.op == 'avey_b'
-
-    def once():
-        return orc.contextualize(z, None if normalize else v, gate, bias, valid, eps=1e-6, norm_eps=1e-12,
-                                 causal=cfg.causal, normalize=normalize, activation='identity', acc=np.float32)
-
-    once()  # warm caches / thread pools
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    return statistics.median(times), cores, len(times)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        def once():
+            return tref.contextualize(inputs_cpu['z_tr'], None if normalize else inputs_cpu['v'],
+                                      inputs_cpu['z_tl'], inputs_cpu['bias'], inputs_cpu['valid'], eps=1e-6,
+                                      norm_eps=1e-12, causal=cfg.causal, normalize=normalize,
+                                      activation='identity')
+        with torch.inference_mode():
+            for _ in range(2):
+                once()
+            times = []
+            t_start = time.perf_counter()
+            while len(times) < 10 or (time.perf_counter() - t_start < 1.0):
+                t0 = time.perf_counter()
+                once()
+                times.append(time.perf_counter() - t0)
+                if time.perf_counter() - t_start > seconds and len(times) >= 3:
+                    break
+        return statistics.median(times), len(times)
+    finally:
+        torch.set_num_threads(prev)
 
 
 def measure_config(torch, wl, tag, steps, warmup, cold_calls):
+    """Warm graph time per call, eager time per call, and the cold kernel estimate."""
     cfg = wl.CONFIGS[tag]
     inp = wl.make_inputs(cfg, device='cuda')
     flops = wl.useful_flops(cfg, inp['valid'])
@@ -164,7 +183,13 @@ def measure_config(torch, wl, tag, steps, warmup, cold_calls):
 
     per_call_ms, wall_ms = measure_graph(torch, fn, steps, warmup)
     eager_ms = measure_eager(torch, fn, max(steps // 4, 10))
-    cold_ms = measure_cold(torch, fn, cold_calls) if cold_calls > 0 else None
+    cold_ms = None
+    if cold_calls > 0:
+        span_cold = measure_single_calls(torch, fn, cold_calls, flush=True)
+        span_warm = measure_single_calls(torch, fn, cold_calls, flush=False)
+        # A negative difference (the kernel hides its HBM fetch) counts as no penalty.
+        cold_ms = per_call_ms + max(span_cold - span_warm, 0.0)
+        SPANS[tag] = (round(span_cold * 1e3, 3), round(span_warm * 1e3, 3))
     return cfg, inp, flops, nbytes, per_call_ms, wall_ms, eager_ms, cold_ms
 
 
@@ -215,15 +240,26 @@ def measure_backward(torch, wl, tag, steps, warmup):
     return row
 
 
-def roofline_block(flops, nbytes, per_call_ms, traffic):
+def roofline_block(flops, nbytes, per_call_ms, traffic, cold_ms=None):
+    """Roofline of one call: HBM-bound below the ridge (compulsory bytes / time),
+    MFMA-bound above it (useful flops / time). `frac_cold` applies the same to the
+    cold (MALL-flushed) kernel time."""
     ai = flops / nbytes
     if ai < RIDGE:
-        achieved = nbytes / (per_call_ms * 1e-3) / 1e9
-        return {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
-                'frac': round(achieved / PEAK_HBM_GBPS, 4), 'traffic': traffic}
-    achieved = flops / (per_call_ms * 1e-3) / 1e12
-    return {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
-            'frac': round(achieved / PEAK_BF16_TFLOPS, 4), 'traffic': traffic}
+        rate = lambda ms: nbytes / (ms * 1e-3) / 1e9
+        block = {'bound': 'hbm', 'achieved': round(rate(per_call_ms), 1), 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s'}
+        peak = PEAK_HBM_GBPS
+    else:
+        rate = lambda ms: flops / (ms * 1e-3) / 1e12
+        block = {'bound': 'mfma', 'achieved': round(rate(per_call_ms), 2), 'peak': PEAK_BF16_TFLOPS,
+                 'unit': 'TFLOP/s'}
+        peak = PEAK_BF16_TFLOPS
+    block['frac'] = round(rate(per_call_ms) / peak, 4)
+    block['traffic'] = traffic
+    if cold_ms is not None:
+        block['achieved_cold'] = round(rate(cold_ms), 2)
+        block['frac_cold'] = round(rate(cold_ms) / peak, 4)
+    return block
 
 
 def load_traffic(tag):
@@ -242,6 +278,21 @@ def load_traffic(tag):
     return None
 
 
+def load_mfma_busy(tag):
+    """Counter-measured MFMA busy percentage (rocprofv3 derived counter MfmaUtil =
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs)) from the committed summary
+    profiles/fused_fwd_counters.md, if present."""
+    root = os.path.dirname(os.path.abspath(__file__))
+    path = os.path.join(root, 'profiles', 'fused_fwd_counters.md')
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        for line in fh:
+            if line.startswith(f'mfma_util_pct {tag}:'):
+                return float(line.split(':', 1)[1])
+    return None
+
+
 def profile_dispatches(torch, wl, tag, n, copy_mib):
     """Launch sequence for rocprofv3 counter runs: one copy of known size, then n calls."""
     src = torch.empty(copy_mib << 20, dtype=torch.uint8, device='cuda').fill_(1)
@@ -257,6 +308,21 @@ def profile_dispatches(torch, wl, tag, n, copy_mib):
     torch.cuda.synchronize()
     log(f'[bench] profiled {n} dispatches of {cfg.name} after a {copy_mib} MiB copy; '
         f'compulsory bytes {wl.compulsory_bytes(cfg)}')
+
+
+def config_row(torch, wl, _hip, tag, steps, warmup, cold_calls):
+    cfg, inp, flops, nbytes, ms, _, eager_ms, cold_ms = measure_config(torch, wl, tag, steps, warmup, cold_calls)
+    row = {'config': cfg.name, 'us_per_call': round(ms * 1e3, 3), 'us_eager': round(eager_ms * 1e3, 3),
+           'us_cold': None if cold_ms is None else round(cold_ms * 1e3, 3),
+           'tflops_useful': round(flops / (ms * 1e-3) / 1e12, 2),
+           'pct_bf16_peak': round(100 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+           'mfma_busy_pct_counter': load_mfma_busy(tag),
+           'roofline': roofline_block(flops, nbytes, ms, load_traffic(tag), cold_ms),
+           'single_call_spans_us_cold_warm': SPANS.get(tag),
+           'plan': _hip.plan(tuple(inp['z_tr'].shape), cfg.dtype, causal=cfg.causal, normalize=cfg.op == 'avey_b')}
+    del inp
+    torch.cuda.empty_cache()
+    return row
 
 
 def main():
@@ -285,45 +351,54 @@ def main():
         torch, wl, args.config, args.steps, args.warmup, args.cold_calls)
     tflops = flops / (per_call_ms * 1e-3) / 1e12
     plan = _hip.plan(tuple(inp['z_tr'].shape), cfg.dtype, causal=cfg.causal, normalize=cfg.op == 'avey_b')
-    log(f'[bench] {cfg.name}: {per_call_ms * 1e3:.2f} us/call (graph), {eager_ms * 1e3:.2f} us/call (eager), '
+    log(f'[bench] {cfg.name}: {per_call_ms * 1e3:.2f} us/call (graph, warm), {eager_ms * 1e3:.2f} us/call (eager), '
         f'cold {cold_ms * 1e3 if cold_ms else float("nan"):.2f} us, {tflops:.1f} TFLOP/s, plan {plan}')
+    del inp
+    torch.cuda.empty_cache()
 
     extra = {
         'us_per_call_graph_warm': round(per_call_ms * 1e3, 3),
         'us_per_call_eager': round(eager_ms * 1e3, 3),
         'us_per_call_cold_mall_flushed': None if cold_ms is None else round(cold_ms * 1e3, 3),
         'tflops_cold': None if cold_ms is None else round(flops / (cold_ms * 1e-3) / 1e12, 2),
+        'cold_method': f'median of {args.cold_calls} single calls after a 512 MiB write, minus the median of '
+                       f'{args.cold_calls} single calls after a 4 KiB write, added to the warm graph time',
+        'single_call_spans_us_cold_warm': SPANS.get(cfg.tag),
         'wall_ms_per_step': round(wall_ms, 5),
         'useful_flops': flops,
         'compulsory_bytes': nbytes,
+        'pct_bf16_peak_useful': round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        'mfma_busy_pct_counter': load_mfma_busy(cfg.tag),
         'plan': plan,
     }
 
     cpu = None
     if not args.no_cpu:
         inputs_cpu = wl.make_inputs(cfg, device='cpu')
-        secs, cores, reps = cpu_baseline(cfg, inputs_cpu, args.cpu_seconds)
-        cpu = {'value': round(flops / secs / 1e12, 5), 'unit': 'TFLOP/s', 'cores': cores, 'kind': 'port',
-               'sample': f'numpy oracle (fp32, dense N x N like ops.py:61-91) on the full {cfg.tag} inputs, '
-                         f'median of {reps} calls = {secs * 1e3:.1f} ms/call; useful-flop rate'}
+        threads = torch.get_num_threads()
+        secs, reps = cpu_baseline(torch, cfg, inputs_cpu, args.cpu_seconds, threads)
+        secs1, reps1 = cpu_baseline(torch, cfg, inputs_cpu, args.cpu_seconds, 1)
+        dense = wl.dense_flops(cfg)
+        cpu = {'value': round(flops / secs / 1e12, 5), 'unit': 'TFLOP/s', 'cores': threads, 'kind': 'port',
+               'sample': f'torch-eager restatement of the reference path (oracle/avey_torch_ref.py, fp32, dense '
+                         f'N x N, inference_mode) on the full {cfg.tag} inputs: median of {reps} calls = '
+                         f'{secs * 1e3:.2f} ms/call at {threads} threads; useful-flop rate',
+               'ms_per_call': round(secs * 1e3, 3), 'ms_per_call_1_thread': round(secs1 * 1e3, 3),
+               'calls_1_thread': reps1,
+               'dense_equiv_tflops': round(dense / secs / 1e12, 5),
+               'dense_equiv_tflops_1_thread': round(dense / secs1 / 1e12, 5),
+               'torch_num_threads': threads, 'affinity_cpus': len(os.sched_getaffinity(0)),
+               'cpu_model': host_cpu_model(),
+               'gpu_speedup_warm': round(secs / (per_call_ms * 1e-3), 1)}
         log(f'[bench] cpu baseline {cpu}')
 
-    all_rows = []
-    if args.all_configs:
+    rows = []
+    if not args.headline_only:
         for tag in wl.CONFIGS:
-            c2, i2, f2, b2, ms2, _, eg2, cold2 = measure_config(torch, wl, tag, max(args.steps // 2, 20),
-                                                                args.warmup, args.cold_calls)
-            row = {'config': c2.name, 'us_per_call': round(ms2 * 1e3, 3), 'us_eager': round(eg2 * 1e3, 3),
-                   'us_cold': None if cold2 is None else round(cold2 * 1e3, 3),
-                   'tflops_useful': round(f2 / (ms2 * 1e-3) / 1e12, 2),
-                   'pct_bf16_peak': round(100 * f2 / (ms2 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
-                   'roofline': roofline_block(f2, b2, ms2, load_traffic(tag)),
-                   'plan': _hip.plan(tuple(i2['z_tr'].shape), c2.dtype, causal=c2.causal,
-                                     normalize=c2.op == 'avey_b')}
-            all_rows.append(row)
+            row = config_row(torch, wl, _hip, tag, max(args.steps // 2, 20), args.warmup, args.cold_calls)
+            rows.append(row)
             log(f'[bench] {json.dumps(row)}')
-            del i2
-            torch.cuda.empty_cache()
+    extra['configs'] = rows
 
     bwd_rows = []
     if args.backward:
@@ -341,7 +416,6 @@ def main():
         'warmup': args.warmup,
         'ms_per_step': round(per_call_ms, 6),
         'us_per_call': round(per_call_ms * 1e3, 3),
-        'mfma_util_pct': round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
@@ -353,13 +427,13 @@ def main():
                    'activation': 'identity', 'parallelism': 'single GPU',
                    'timing': f'one HIP graph of {args.steps} back-to-back calls; HIP events on the launch stream',
                    'flops': 'useful: 4*D*allowed pairs'},
-        'roofline': roofline_block(flops, nbytes, per_call_ms, load_traffic(cfg.tag)),
+        'roofline': roofline_block(flops, nbytes, per_call_ms, load_traffic(cfg.tag), cold_ms),
         'cpu_baseline': cpu,
         'extra': extra,
     }
     if args.report:
         with open(args.report, 'w') as fh:
-            json.dump({'headline': line, 'configs': all_rows, 'backward': bwd_rows}, fh, indent=1)
+            json.dump({'headline': line, 'backward': bwd_rows}, fh, indent=1)
     print(json.dumps(line), flush=True)
 
 

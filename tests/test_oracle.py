@@ -280,3 +280,33 @@ def test_row_condition_matches_a_loop_over_keys():
             s = [0.0 if not (valid[b, i] and valid[b, j]) else
                  float(zi @ z[b, j]) / (np.linalg.norm(zi) * np.linalg.norm(z[b, j])) for j in range(9)]
             assert abs(got[b, i] - sum(map(abs, s)) / abs(sum(s) + 0.1)) < 1e-12 * (1 + got[b, i])
+
+
+@pytest.mark.parametrize('causal,normalize,use_v,act', [
+    (True, False, True, 'identity'), (False, False, True, 'silu'), (False, True, False, 'gelu'),
+    (False, True, False, 'relu2'), (True, False, False, 'relu')])
+def test_torch_restatement_matches_numpy_oracle(causal, normalize, use_v, act):
+    # oracle/avey_torch_ref.py (the CPU baseline bench.py times) against the numpy
+    # oracle, in fp64 (agreement to rounding) and in fp32 / bf16 storage.
+    from oracle import avey_torch_ref as tref
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(3, 19, 12, generator=g, dtype=torch.float64)
+    gate = torch.randn(3, 19, 12, generator=g, dtype=torch.float64)
+    bias = torch.randn(12, generator=g, dtype=torch.float64)
+    v = torch.randn(19, 19, generator=g, dtype=torch.float64) if use_v else None
+    valid = torch.rand(3, 19, generator=g) > 0.25
+    z[~valid] = float('nan')
+    kw = dict(eps=0.5, norm_eps=1e-12, causal=causal, normalize=normalize, activation=act)
+    want = orc.contextualize(z.numpy(), None if v is None else v.numpy(), gate.numpy(), bias.numpy(),
+                             valid.numpy(), acc=np.float64, **kw)
+    got = tref.contextualize(z, v, gate, bias, valid, **kw)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+    for dt in (torch.float32, torch.bfloat16):
+        zz, gg, bb = (t.to(dt) for t in (z, gate, bias))
+        vv = None if v is None else v.to(dt)
+        got = tref.contextualize(zz, vv, gg, bb, valid, **kw)
+        assert got.dtype == dt
+        want = orc.contextualize(zz.double().numpy(), None if vv is None else vv.double().numpy(),
+                                 gg.double().numpy(), bb.double().numpy(), valid.numpy(), acc=np.float32, **kw)
+        tol = 1e-5 if dt == torch.float32 else 1e-2
+        np.testing.assert_allclose(got.double().numpy(), want, rtol=tol, atol=tol)
