@@ -64,6 +64,7 @@ class AveyFwdPlan(ctypes.Structure):
 # Symbols of include/avey_hip.h with their ctypes signatures.
 EXPORTS = {
     'avey_fwd': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    'avey_fwd_noalloc': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.c_void_p]),
     'avey_fwd_workspace_bytes': (ctypes.c_int64, [ctypes.POINTER(AveyFwdArgs)]),
     'avey_fwd_plan': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.POINTER(AveyFwdPlan)]),
     'avey_key_tile_count': (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
@@ -75,7 +76,8 @@ EXPORTS = {
     'avey_abi_version': (ctypes.c_int, []),
     'avey_debug_poison_lds': (ctypes.c_int, [ctypes.c_void_p]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
+NOALLOC_SCRATCH_BYTES = 4 << 20  # AVEY_NOALLOC_SCRATCH_BYTES of include/avey_hip.h
 
 _lib = None
 

@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "avey_common.h"
 #include "avey_internal.h"
@@ -14,6 +15,27 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_device_ok[kMaxDevices];  // 0 unknown, 1 gfx950, 2 other
+
+// Scratch of the allocation-free entry point (avey_fwd_noalloc): one copy of this
+// array per GPU, for the life of the process. Host code never uses its name as an
+// address (on the host it is only a stand-in for the symbol); the device address of
+// each GPU's copy comes from hipGetSymbolAddress, once per device, with that device
+// current, and is kept in g_scratch.
+static __device__ __align__(256) char scratch[AVEY_NOALLOC_SCRATCH_BYTES];
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// Device address of `dev`'s copy of the scratch array; `dev` must be current.
+hipError_t device_scratch(int dev, void** ptr) {
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
+  *ptr = slot.err == hipSuccess ? slot.ptr : nullptr;
+  return slot.err;
+}
 
 size_t elem_size(int dtype) {
   switch (dtype) {
@@ -208,6 +230,8 @@ const char* avey_status_string(int status) {
     case AVEY_ERR_FLAGS: return "causal and normalize must be 0 or 1";
     case AVEY_ERR_ALIAS: return "out overlaps an input buffer";
     case AVEY_ERR_STRIDE: return "z_tr / z_tl row stride below features, or a negative stride";
+    case AVEY_ERR_SCRATCH:
+      return "the call needs more scratch than avey_fwd_noalloc holds (AVEY_NOALLOC_SCRATCH_BYTES)";
     case AVEY_ERR_UNSUPPORTED:
       return "backward needs bf16 / fp16 / fp32, features <= 1024, batch <= 65535 and contiguous operands";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
@@ -320,16 +344,11 @@ int avey_bwd(const avey_bwd_args* a, void* workspace, size_t workspace_bytes, vo
   return e == hipSuccess ? AVEY_OK : (int)e;
 }
 
-int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
-  const int st = validate(a);
-  if (st != AVEY_OK) return st;
-  const Plan pl = make_plan(*a);
-  if (pl.work_bytes > 0 && (!workspace || workspace_bytes < (size_t)pl.work_bytes)) return AVEY_ERR_WORKSPACE;
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return (int)e;
-  if (!device_ok(dev)) return AVEY_ERR_DEVICE;
+}  // extern "C"
 
+namespace {
+// Launches the planned kernels of a validated call with `work` as their scratch.
+int run_fwd(const avey_fwd_args* a, const Plan& pl, void* work, hipStream_t s) {
   FwdParams p{};
   p.z = a->z_tr;
   p.v = a->v;
@@ -337,7 +356,7 @@ int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, vo
   p.bias = a->bias;
   p.valid = a->valid;
   p.out = a->out;
-  p.work = workspace;
+  p.work = work;
   p.B = a->batch;
   p.C = a->context;
   p.D = a->features;
@@ -352,10 +371,44 @@ int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, vo
   p.act = a->activation;
   p.eps = a->eps;
   p.norm_eps = a->norm_eps;
-
-  hipStream_t s = (hipStream_t)stream;
-  e = pl.kernel == 1 ? launch_fused(p, a->dtype, pl, s) : launch_generic(p, a->dtype, pl, s);
+  const hipError_t e = pl.kernel == 1 ? launch_fused(p, a->dtype, pl, s) : launch_generic(p, a->dtype, pl, s);
   return e == hipSuccess ? AVEY_OK : (int)e;
+}
+
+// The current device, checked to be a gfx950 GPU.
+int current_device(int* dev) {
+  const hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return (int)e;
+  return device_ok(*dev) ? AVEY_OK : AVEY_ERR_DEVICE;
+}
+}  // namespace
+
+extern "C" {
+
+int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = validate(a);
+  if (st != AVEY_OK) return st;
+  const Plan pl = make_plan(*a);
+  if (pl.work_bytes > 0 && (!workspace || workspace_bytes < (size_t)pl.work_bytes)) return AVEY_ERR_WORKSPACE;
+  int dev = -1;
+  const int ds = current_device(&dev);
+  if (ds != AVEY_OK) return ds;
+  return run_fwd(a, pl, workspace, (hipStream_t)stream);
+}
+
+int avey_fwd_noalloc(const avey_fwd_args* a, void* stream) {
+  const int st = validate(a);
+  if (st != AVEY_OK) return st;
+  const Plan pl = make_plan(*a);
+  if (pl.work_bytes > (int64_t)AVEY_NOALLOC_SCRATCH_BYTES) return AVEY_ERR_SCRATCH;
+  int dev = -1;
+  const int ds = current_device(&dev);
+  if (ds != AVEY_OK) return ds;
+  // The first call on a device looks up that device's copy of the scratch array.
+  void* work = nullptr;
+  const hipError_t e = device_scratch(dev, &work);
+  if (e != hipSuccess) return (int)e;
+  return run_fwd(a, pl, work, (hipStream_t)stream);
 }
 
 }  // extern "C"

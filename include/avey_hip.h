@@ -14,6 +14,8 @@
  *                         static, documented tile table; host-only, no GPU needed.
  *   - avey_key_tile_count replaces `_key_tile_count` (avey_kernels/_triton.py:38-50),
  *                         the causal tile-skip rule; host-only.
+ *   - avey_fwd_noalloc    avey_fwd without allocation; no reference counterpart
+ *                         (for callers that cannot allocate device memory).
  *   - avey_bwd            replaces autograd over the eager path for the
  *                         gradients (avey_kernels/ops.py:96-106 and :61-91).
  *   - avey_fwd_workspace_bytes, avey_bwd_workspace_bytes, avey_status_string, avey_abi_version,
@@ -45,7 +47,7 @@
 extern "C" {
 #endif
 
-#define AVEY_ABI_VERSION 3
+#define AVEY_ABI_VERSION 4
 
 /* Element type of z_tr / z_tl / v / bias / out. */
 enum avey_dtype {
@@ -77,6 +79,7 @@ enum avey_status {
   AVEY_ERR_ALIAS = -9,            /* out overlaps an input */
   AVEY_ERR_STRIDE = -10,          /* a row stride below features, or a negative stride */
   AVEY_ERR_UNSUPPORTED = -11,     /* backward: fp64, features > 1024, batch > 65535 or strided operands */
+  AVEY_ERR_SCRATCH = -12,         /* avey_fwd_noalloc: the call needs more than AVEY_NOALLOC_SCRATCH_BYTES */
 };
 
 typedef struct avey_fwd_args {
@@ -135,6 +138,18 @@ typedef struct avey_fwd_plan_t {
 /* Launch the forward contextualizer on `stream` (a hipStream_t; NULL = default stream). */
 int avey_fwd(const avey_fwd_args* args, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The forward without allocation (ABI 4). No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP-graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels
+ * and results as avey_fwd; the scratch the kernels need (the generic fp32 / fp64
+ * kernel's per-row inverse norms, 4 or 8 bytes per batch x context row; the fused
+ * bf16 / fp16 kernels need none) comes from a static device array of
+ * AVEY_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends. It calls
+ * no hipMalloc / hipFree. Larger needs return AVEY_ERR_SCRATCH. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other
+ * host threads) race and must be serialised by the caller. */
+#define AVEY_NOALLOC_SCRATCH_BYTES (4u << 20)
+int avey_fwd_noalloc(const avey_fwd_args* args, void* stream);
 /* Device scratch bytes avey_fwd needs for these arguments (0 when none). Host-only. */
 int64_t avey_fwd_workspace_bytes(const avey_fwd_args* args);
 

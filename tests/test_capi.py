@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_hip.EXPORTS), declared ^ set(_hip.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.avey_abi_version() == _hip.ABI_VERSION == 3
+    assert lib.avey_abi_version() == _hip.ABI_VERSION == 4
 
 
 def _args(**over):
@@ -67,6 +67,7 @@ def test_argument_errors_return_status_before_any_device_work(over, code):
     lib = _lib()
     args = _args(**over)
     assert lib.avey_fwd(ctypes.byref(args), None, 0, None) == code
+    assert lib.avey_fwd_noalloc(ctypes.byref(args), None) == code
     assert lib.avey_fwd_plan(ctypes.byref(args), ctypes.byref(_hip.AveyFwdPlan())) == code
     assert lib.avey_fwd_workspace_bytes(ctypes.byref(args)) == -1
     assert lib.avey_status_string(code).decode() not in ('', 'unknown status')
@@ -187,3 +188,18 @@ def test_row_strides_of_torch_views():
     assert _hip.row_strides(x[..., 8:]) == (16, 80)
     with pytest.raises(ValueError):
         _hip.row_strides(x.transpose(1, 2))
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch_before_any_device_work():
+    # The generic fp32 kernel needs 4 bytes of scratch per (batch, context) row: 2 x
+    # 600000 rows need 4.8 MB, past the 4 MiB static array of avey_fwd_noalloc.
+    lib = _lib()
+    assert _hip.NOALLOC_SCRATCH_BYTES == 4 << 20
+    big = _args(dtype=0, context=600000)
+    assert lib.avey_fwd_workspace_bytes(ctypes.byref(big)) == 2 * 600000 * 4
+    assert lib.avey_fwd_noalloc(ctypes.byref(big), None) == -12
+    assert 'AVEY_NOALLOC_SCRATCH_BYTES' in lib.avey_status_string(-12).decode()
+    # At the limit the size check passes (the call then goes on to the device check).
+    fits = _args(dtype=0, batch=1, context=(4 << 20) // 4)
+    assert lib.avey_fwd_workspace_bytes(ctypes.byref(fits)) == 4 << 20
+    assert lib.avey_fwd_noalloc(ctypes.byref(fits), None) != -12
