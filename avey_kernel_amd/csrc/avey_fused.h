@@ -27,12 +27,8 @@
 // partials; the key tiles sit in a ring of 2 or 3 LDS slots, refilled by
 // buffer-to-LDS copies a tile or two ahead.
 //
-// Waves per workgroup (fused_threads in avey_common.h):
-//   * 16-row variants, 8 waves ("warp specialization"): waves 0-3 do A, C and T,
-//     waves 4-7 ("helpers", one per feature slice) do B, the V loads, the key norm
-//     reciprocals and the key-tile copies, in a program of their own that passes the
-//     same barriers. Each SIMD holds a product wave and a helper wave, and the
-//     reduction and the memory traffic no longer stall the MFMAs.
+// Waves per workgroup (fused_threads in avey_common.h; 16-row blocks run the
+// role-split kernel of avey_fused16.h instead):
 //   * 32-row variants and 64-row ones up to 128 features per slice, 8 waves ("query
 //     split"): waves w and w+4 serve slice w, each for half of the query blocks, so
 //     each holds half the accumulators. Each copies half of a key tile's rows and
@@ -246,20 +242,13 @@ struct Geo {
   static constexpr int R = 3 * TILE + OVF + SMALL <= kLdsMax ? 3 : 2;
   static_assert(2 * TILE + OVF + SMALL <= kLdsMax, "tile does not fit the LDS");
   static_assert(BM <= 32 * R, "query rows must fit the ring");
-  // Warp specialization (16-row variants, whose waves fit 256 registers): 8 waves,
-  // waves 0-3 run the products on their feature slices as in the 4-wave kernel,
-  // waves 4-7 ("helpers", helper h for slice h) run the reduction, the V loads, the
-  // key reciprocals and the refill DMAs, so that none of these stalls the MFMAs, and
-  // each SIMD holds two waves whose stalls the other fills.
-  static constexpr bool WS = BM == 16;
   // Query split (the 32- and 64-row variants whose halved state fits 256 registers):
   // 8 waves, waves w and w + 4 both serve feature slice w, each for half of the query
   // blocks. Every wave runs every stage on its half (the key rows of a slice are read
   // by both), so a wave holds half the accumulators and each SIMD holds two waves
   // whose stalls the other fills. The others keep 4 waves of 512 registers.
   static constexpr bool QS = fused_query_split(BM, NK);
-  static constexpr int THREADS = fused_threads(BM, NK);
-  static_assert(THREADS == (WS || QS ? 2 : 1) * kThreads, "wave count");
+  static constexpr int THREADS = (QS ? 2 : 1) * kThreads;
   static constexpr int QBW = QS ? QB / 2 : QB;        // query blocks per wave
   static constexpr int KD = QS ? KDMA / 2 : KDMA;     // refill copies per wave per tile
 };
@@ -319,7 +308,8 @@ __device__ __forceinline__ void wait_lds_reads() { __builtin_amdgcn_s_waitcnt(0x
 template <typename T16, int BM, int NK, bool FULL, bool STRIDED, bool HILO>
 __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(FwdParams p) {
   typedef Geo<BM, NK> Gm;
-  constexpr bool WS = Gm::WS, QS = Gm::QS;
+  static_assert(BM > 16 && Gm::THREADS == fused_threads(BM, NK), "16-row blocks run fused16_kernel");
+  constexpr bool QS = Gm::QS;
   constexpr int QB = Gm::QB, DS = Gm::DS, NT = Gm::NT, CPR = Gm::CPR, CPRP = Gm::CPRP, G = Gm::G;
   constexpr int SLICE = Gm::SLICE, TILE = Gm::TILE, R = Gm::R, KDMA = Gm::KDMA;
   constexpr int QBW = Gm::QBW, KD = Gm::KD;
@@ -344,12 +334,9 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // from it (DMA destinations go through M0) stay scalar.
   const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
-  // w: the feature slice this wave serves; helper: a warp-specialized helper wave
-  // (helpers branch off into a loop of their own before the first key tile); h:
-  // the query half of a query-split wave, whose query blocks are qb0 .. qb0+QBW-1.
-  const int w = (WS || QS) ? (wv & (kWaves - 1)) : wv;
-  const bool helper = WS && wv >= kWaves;
-  const bool do_mma = !helper;
+  // w: the feature slice this wave serves; h: the query half of a query-split wave,
+  // whose query blocks are qb0 .. qb0+QBW-1.
+  const int w = QS ? (wv & (kWaves - 1)) : wv;
   const int h = QS ? (wv >> 2) : 0;
   const int qb0 = h * QBW;
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
@@ -488,7 +475,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // (they are then live for less of the iteration, which the 64-row variants'
   // registers need), before them by the others (the query-split waits count the
   // copies as the newest loads).
-  constexpr bool VALID_LATE = !QS && !WS;
+  constexpr bool VALID_LATE = !QS;
   auto fetch_key_share = [&](int t, char* dst, int jj, const uint32_t (&kof)[P], bool live) {
     if constexpr (QS)
       dma16(rows_rsrc(zb, t * kBN + RPP * h, live ? C : 0, zstride, row_bytes), dst + 1024 * (h * KD + jj), kof[jj]);
@@ -536,25 +523,10 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
 
   // ---- prologue: the query rows, the first R-1 key tiles, the query norms ------------
-  // In the warp-specialized variants the helpers copy tiles 0 and 1 (first thing in
-  // their program; tile 0 is then ordered for the product waves by their wait and a
-  // barrier before A(0)), so that the product waves issue only the query rows and
-  // reach the query norms early; the product waves still load the tiles' validity
-  // bytes, which they use.
-  if (do_mma) {
-    fetch_rows((const char*)zb, zstride, qrows_base);
-    if constexpr (WS)
-      fetch_valid(0, IC<0>{});
-    else
-      fetch_keys(0, IC<0>{});
-    if constexpr (R == 3) {
-      if (1 < nkt) {
-        if constexpr (WS)
-          fetch_valid(1, IC<1>{});
-        else
-          fetch_keys(1, IC<1>{});
-      }
-    }
+  fetch_rows((const char*)zb, zstride, qrows_base);
+  fetch_keys(0, IC<0>{});
+  if constexpr (R == 3) {
+    if (1 < nkt) fetch_keys(1, IC<1>{});
   }
   // The gate rows are first read in the tail; one touch per 128-byte line ahead of
   // that brings them into the L2, so that their fetch does not wait on HBM. When the
@@ -576,10 +548,10 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
   };
   // (Query split: after the first barrier, which waits for every copy before it.)
-  if (!QS && do_mma && has_gate && touch_t < 1) touch_gate();
+  if (!QS && has_gate && touch_t < 1) touch_gate();
   // Query fragments of this wave's query blocks (local index qb: block qb0 + qb).
   u32x4 qf[QBW][NK];
-  if (do_mma) {
+  {
   uint32_t qv[QBW];
 #pragma unroll
   for (int qb = 0; qb < QBW; ++qb)
@@ -779,23 +751,6 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
   };
 
-  // ---- warp-specialized refill: a helper copies key tile tf into its slice of slot F,
-  // copies [j0, j1) of KDMA. Issuing them is throttled by the CU's memory pipe (about
-  // 50 cycles per copy with four helpers issuing), so with three slots a steady-state
-  // iteration splits them: the first half after the reduction (the product waves run
-  // A meanwhile), the second after the key reciprocals (they run C and T); with two
-  // slots all go out after the reduction, as they must land within the iteration.
-  // The product waves cannot
-  // wait for another wave's copies: the helper's wait and the next barrier are what
-  // orders their reads after a copy. With three slots a refill is read two barriers
-  // pairs later, so the wait at an iteration's end retires the previous iteration's
-  // refill and leaves this one in flight; with two slots it retires everything. -----
-  auto refill_part = [&](int tf, auto fslot, auto j0, auto j1) {
-    uint32_t kof[P];
-    key_offsets(kof);
-#pragma unroll
-    for (int j = decltype(j0)::value; j < decltype(j1)::value; ++j) fetch_key_part(tf, slot_base(fslot), j, kof);
-  };
   // s_waitcnt encodings (gfx9: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at
   // their maxima, i.e. not waited for).
   static_assert(KDMA + 2 < 64, "vmcnt holds 6 bits");
@@ -805,8 +760,6 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     constexpr int N = decltype(n)::value;
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   };
-  // The refill just issued (KDMA copies) may stay in flight.
-  auto wait_keep_refill = [&]() { wait_keep(IC<KDMA>{}); };
   // Query split: each wave of a slice copies half of a key tile's rows and reads them
   // all, so a wave's copies are ordered before its partner's reads by its own wait and
   // a barrier. Before the barrier that closes iteration t, key tile t+1 has landed:
@@ -830,7 +783,8 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   // t = 0: A only (with the whole fetch of the last tile of the ring's first round);
   // the query norms, A(0)'s publication and tile 0's mixing operands. The query rows
   // share slot R-1 with that tile; their reads into qf are complete (the norms above
-  // consumed them) before the refill is issued (after the barrier, by a helper).
+  // consumed them) before the refill is issued (after the wave's LDS reads retired;
+  // query split: after a barrier, as the partner read them too).
   // Steady-state iterations run over t = 1 .. nkt-1, unrolled by R so that every slot
   // index is a constant.
   auto run_loop = [&](auto iter) {
@@ -853,59 +807,6 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
   using TT = std::true_type;
   using FF = std::false_type;
-  if constexpr (WS) {
-    if (helper) {
-      // The helpers' program: the same barriers as the product waves', in order.
-      // Copies issued before the reduction's barrier. With two slots the refill must
-      // land by the end of its own iteration, so all of it goes out early.
-      constexpr int KH = R == 2 ? KDMA : KDMA / 2;
-      refill_part(0, IC<0>{}, IC<0>{}, IC<KDMA>{});  // tiles 0 and 1 (see the prologue)
-      if (R == 3 && 1 < nkt) {
-        refill_part(1, IC<1>{}, IC<0>{}, IC<KDMA>{});
-        wait_keep_refill();
-      } else {
-        wait_all();
-      }
-      lds_barrier();  // tile 0 has landed; the query rows in slot R-1 are consumed
-      load_v(0, vv);
-      if (R - 1 < nkt) refill_part(R - 1, IC<R - 1>{}, IC<0>{}, IC<KDMA>{});
-      lds_barrier();  // A(0) done
-      publish(FF{}, TT{});
-      // Tile 1 lands before iteration 1; with three slots tile 2 may stay in flight.
-      if (R == 3 && R - 1 < nkt)
-        wait_keep_refill();
-      else
-        wait_all();
-      lds_barrier();
-      run_loop([&](int t, auto cur) {
-        constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
-        const bool refill = t + R - 1 < nkt;
-        // The V words B consumes were loaded an iteration ago.
-        stage_b(t - 1);
-        if (refill) refill_part(t + R - 1, IC<PREV>{}, IC<0>{}, IC<KH>{});
-        lds_barrier();
-        publish(FF{}, TT{});
-        if (refill) refill_part(t + R - 1, IC<PREV>{}, IC<KH>{}, IC<KDMA>{});
-        if (R == 3 && refill)
-          wait_keep_refill();
-        else
-          wait_all();
-        lds_barrier();
-      });
-      stage_b(nkt - 1);
-      lds_barrier();
-      if (p.normalize) {
-#pragma unroll
-        for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
-        lds_barrier();
-        lds_barrier();
-      }
-      return;
-    }
-  }
-  // From here on: the product waves (all waves without warp specialization).
-  constexpr bool RED = !WS;
-  using RT = std::integral_constant<bool, RED>;
   if constexpr (QS) {
     // Key tile 0 (and 1) from both waves of the slice; the partner's query reads done
     // before this wave's refill overwrites slot R-1.
@@ -913,15 +814,10 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     lds_barrier();
     if (has_gate && touch_t < 1) touch_gate();
   }
-  if constexpr (WS) lds_barrier();  // the helpers' copy of tile 0
-  if constexpr (RED) load_v(0, vv);
+  load_v(0, vv);
   wait_lds_reads();
   if constexpr (!VALID_LATE) fetch_valid(R - 1, IC<R - 1>{}, R - 1 < nkt);
-  if constexpr (WS) {
-    stage_a(0, IC<0>{}, 0, IC<R - 1>{}, false, IC<0>{});
-  } else {
-    stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KD>{});
-  }
+  stage_a(0, IC<0>{}, R - 1, IC<R - 1>{}, R - 1 < nkt, IC<KD>{});
   lds_barrier();
   if (tid < BM) {
     float ss = 0.f;
@@ -930,7 +826,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     // F.normalize divides by max(||q||, norm_eps); 0 marks padded / out-of-range rows.
     sm.rq[tid] = ss < 0.f ? 0.f : (ss > eps2 ? __builtin_amdgcn_rsqf(ss) : inv_eps);
   }
-  publish(TT{}, RT{});
+  publish(TT{}, TT{});
   if constexpr (SPLIT) stage_t(IC<0>{});
   if constexpr (QS) wait_next_tile(nkt == 1);
   lds_barrier();
@@ -942,20 +838,6 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   auto iteration = [&](int t, auto cur) {
     constexpr int I = decltype(cur)::value, PREV = (I + R - 1) % R;
     const bool refill = t + R - 1 < nkt;
-    if constexpr (WS) {
-      static_assert(!WS || SPLIT, "warp specialization keeps T at the end of the iteration");
-      // The helpers run B and the refill meanwhile (see their program above).
-      if (has_gate && t == touch_t) touch_gate();
-      fetch_valid(t + R - 1, IC<PREV>{}, refill);
-      stage_a(t, cur, 0, IC<PREV>{}, false, IC<0>{});
-      lds_barrier();
-      stage_c(0, IC<PREV>{}, false, FF{});
-      publish(TT{}, FF{});
-      __builtin_amdgcn_sched_barrier(0);
-      stage_t(cur);
-      lds_barrier();
-      return;
-    }
     if constexpr (!SPLIT) stage_t(IC<PREV>{});
     // The V words B consumes were loaded an iteration ago.
     stage_b(t - 1);
@@ -1003,7 +885,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     for (int qb = 0; qb < QBW; ++qb)
       qv2[qb] = ld8(rows_rsrc(vb, q0 + 16 * (qb0 + qb), valid_rows, 1u, 1u), (uint32_t)li);
   }
-  if constexpr (RED) stage_b(nkt - 1);
+  stage_b(nkt - 1);
   lds_barrier();
   stage_c(0, IC<0>{}, false, FF{});
 
@@ -1017,10 +899,8 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   };
   float rden[QBW];
   if (p.normalize) {
-    if constexpr (RED) {
 #pragma unroll
-      for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
-    }
+    for (int j = 0; j < UPW; ++j) sm.dx[pq[j]][uk[j]][lg][li] = den[j];
     lds_barrier();
     if (tid < BM) {
       float d = 0.f;
