@@ -95,6 +95,25 @@ __host__ __device__ constexpr int fused_threads(int bm, int nk) {
   return (bm == 16 || fused_query_split(bm, nk)) ? 512 : 256;
 }
 
+// Block -> (batch item, query tile) of the fused kernels. Blocks are dispatched
+// round-robin over the 8 XCDs (block i to XCD i % 8), each with its own L2.
+// * Causal grids go heaviest query tile first over the whole grid, and consecutive
+//   blocks walk the batch, so all query tiles of an item share an XCD when B % 8 == 0.
+// * Bidirectional grids (every query tile the same work) with B % 8 == 0 place the
+//   n_qt tiles of an item 8 blocks apart: they share an XCD and are dispatched
+//   together, so the item's key tiles are read from that L2 by all of its query tiles
+//   at about the same time, also when the grid takes more than one round.
+__device__ __forceinline__ void block_item(int i, int B, int n_qt, bool causal, int& b, int& qt) {
+  if (!causal && (B & 7) == 0) {
+    const int r = i >> 3, g = r / n_qt, k = r - g * n_qt;
+    b = 8 * g + (i & 7);
+    qt = n_qt - 1 - k;
+  } else {
+    b = i % B;
+    qt = n_qt - 1 - i / B;
+  }
+}
+
 // Key tiles a query tile visits. Causal skipping keeps the tile holding the
 // diagonal and drops every tile that starts after the block's last query
 // (the reference rule, avey_kernels/_triton.py:38-50).

@@ -46,10 +46,11 @@
 // address is clamped and no load sits under a branch.
 //
 // Key tiles strictly after a query tile's last row are never visited in causal
-// mode (the diagonal tile is kept and masked elementwise). Blocks are numbered
-// heaviest query tile first, and consecutive blocks walk the batch so that all
-// query tiles of one batch item land on the same XCD (its L2 then serves the
-// repeated key reads) whenever the batch is a multiple of 8.
+// mode (the diagonal tile is kept and masked elementwise). The block order
+// (block_item in avey_common.h) puts all query tiles of one batch item on the same
+// XCD whenever the batch is a multiple of 8 (its L2 then serves the repeated key
+// reads): heaviest query tile first in causal mode, and the tiles of an item
+// dispatched together otherwise.
 //
 // Key order along the mixing reduction axis: a 32-key tile is split in halves
 // kb = 0, 1; lane group g (lanes 16g..16g+15) holds keys 4g..4g+3 of each half,
@@ -341,8 +342,8 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
   const int qb0 = h * QBW;
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
   const int n_qt = (C + BM - 1) / BM;
-  const int b = (int)blockIdx.x % B;
-  const int qt = n_qt - 1 - (int)blockIdx.x / B;
+  int b, qt;
+  block_item((int)blockIdx.x, B, n_qt, p.causal != 0, b, qt);
   const int q0 = qt * BM;
   const uint32_t row_bytes = (uint32_t)D * 2u;
   // z_tr and z_tl may be strided views (rows and batch items `*stride` apart).

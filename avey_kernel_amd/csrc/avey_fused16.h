@@ -126,8 +126,8 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
   const int h = wv & 3;                         // M-wave: feature slice
   const int C = (int)p.C, D = (int)p.D, B = (int)p.B;
   const int n_qt = (C + 15) / 16;
-  const int b = (int)blockIdx.x % B;
-  const int qt = n_qt - 1 - (int)blockIdx.x / B;
+  int b, qt;
+  block_item((int)blockIdx.x, B, n_qt, p.causal != 0, b, qt);
   const int q0 = qt * 16;
   const uint32_t row_bytes = (uint32_t)D * 2u;
   const uint32_t zstride = STRIDED ? (uint32_t)p.zrs * 2u : row_bytes;
