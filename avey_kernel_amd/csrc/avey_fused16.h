@@ -81,6 +81,53 @@ __device__ __forceinline__ void copy16(const u32x4s& rs, char* lds, uint32_t off
 __device__ __forceinline__ void copy4(const u32x4s& rs, char* lds, uint32_t off) {
   asm volatile("buffer_load_dword %0, %1, 0 offen lds" : : "v"(off), "s"(rs), "{m0}"(lds_addr(lds)) : "memory");
 }
+// P copies of 1 KB (lane l's 16 bytes to lds + 1024 j + 16 l, j < P) when `real`,
+// else P 4-byte copies of the same lanes into `sink` (a word no one reads). One inline
+// asm block with one branch: every path through it issues exactly P vector-memory
+// operations, so a wait counting them holds whichever way the branch went.
+#define AVEY_CP(j) "buffer_load_dwordx4 %[o" #j "], %[rs], 0 offen lds\n\ts_add_u32 m0, m0, 0x400\n\t"
+#define AVEY_PD(j) "buffer_load_dword %[o" #j "], %[rs], 0 offen lds\n\t"
+#define AVEY_HEAD "s_cmp_eq_u32 %[r], 0\n\ts_cbranch_scc1 1f\n\t"
+#define AVEY_MID "s_branch 2f\n1:\n\ts_mov_b32 m0, %[sink]\n\t"
+template <int P>
+__device__ __forceinline__ void copies_or_pads(uint32_t real, const u32x4s& rs, char* lds, char* sink,
+                                               const uint32_t (&o)[P]) {
+  uint32_t m0 = lds_addr(lds);
+  const uint32_t r = __builtin_amdgcn_readfirstlane(real), sk = lds_addr(sink);
+  if constexpr (P == 2) {
+    asm volatile(AVEY_HEAD AVEY_CP(0) AVEY_CP(1) AVEY_MID AVEY_PD(0) AVEY_PD(1) "2:"
+                 : "+{m0}"(m0)
+                 : [o0] "v"(o[0]), [o1] "v"(o[1]), [rs] "s"(rs), [r] "s"(r), [sink] "s"(sk)
+                 : "memory", "scc");
+  } else if constexpr (P == 4) {
+    asm volatile(AVEY_HEAD AVEY_CP(0) AVEY_CP(1) AVEY_CP(2) AVEY_CP(3) AVEY_MID AVEY_PD(0) AVEY_PD(1) AVEY_PD(2)
+                     AVEY_PD(3) "2:"
+                 : "+{m0}"(m0)
+                 : [o0] "v"(o[0]), [o1] "v"(o[1]), [o2] "v"(o[2]), [o3] "v"(o[3]), [rs] "s"(rs), [r] "s"(r),
+                   [sink] "s"(sk)
+                 : "memory", "scc");
+  } else if constexpr (P == 6) {
+    asm volatile(AVEY_HEAD AVEY_CP(0) AVEY_CP(1) AVEY_CP(2) AVEY_CP(3) AVEY_CP(4) AVEY_CP(5) AVEY_MID AVEY_PD(0)
+                     AVEY_PD(1) AVEY_PD(2) AVEY_PD(3) AVEY_PD(4) AVEY_PD(5) "2:"
+                 : "+{m0}"(m0)
+                 : [o0] "v"(o[0]), [o1] "v"(o[1]), [o2] "v"(o[2]), [o3] "v"(o[3]), [o4] "v"(o[4]), [o5] "v"(o[5]),
+                   [rs] "s"(rs), [r] "s"(r), [sink] "s"(sk)
+                 : "memory", "scc");
+  } else {
+    static_assert(P == 8, "copies per slice");
+    asm volatile(AVEY_HEAD AVEY_CP(0) AVEY_CP(1) AVEY_CP(2) AVEY_CP(3) AVEY_CP(4) AVEY_CP(5) AVEY_CP(6) AVEY_CP(7)
+                     AVEY_MID AVEY_PD(0) AVEY_PD(1) AVEY_PD(2) AVEY_PD(3) AVEY_PD(4) AVEY_PD(5) AVEY_PD(6)
+                         AVEY_PD(7) "2:"
+                 : "+{m0}"(m0)
+                 : [o0] "v"(o[0]), [o1] "v"(o[1]), [o2] "v"(o[2]), [o3] "v"(o[3]), [o4] "v"(o[4]), [o5] "v"(o[5]),
+                   [o6] "v"(o[6]), [o7] "v"(o[7]), [rs] "s"(rs), [r] "s"(r), [sink] "s"(sk)
+                 : "memory", "scc");
+  }
+}
+#undef AVEY_CP
+#undef AVEY_PD
+#undef AVEY_HEAD
+#undef AVEY_MID
 
 // LDS geometry of the 16-row role-split kernel for slices of 32*NK features.
 template <int NK>
@@ -176,13 +223,15 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
       return *reinterpret_cast<const u32x4*>(slice_base + a1[s % (G / 4)] + 16 * (16 * row16 * CPRP + G * (s / (G / 4))));
     };
     // Key tile t, rows 16 kbs .. 16 kbs + 15 of both slices, into ring slot I.
+    // Tiles at or past nkt (the causal limit, or past the context) are copies of nothing:
+    // 4-byte loads through an empty resource into the never-read word, one per copy a
+    // tile would take.
     auto copy_tile = [&](int t, auto slot) {
       char* base = slot_ptr(slot);
-      const u32x4s r = rows_desc(zb, t * kBN + 16 * kbs, C, zstride, row_bytes);
+      const u32x4s r = rows_desc(zb, t * kBN + 16 * kbs, t < nkt ? C : 0, zstride, row_bytes);
+      const uint32_t real = t < nkt ? 1u : 0u;
 #pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int j = 0; j < P; ++j) copy16(r, base + (sl0 + e) * SLICE + 1024 * (kbs * P + j), kof[e][j]);
+      for (int e = 0; e < 2; ++e) copies_or_pads<P>(real, r, base + (sl0 + e) * SLICE + 1024 * kbs * P, touch_sink, kof[e]);
     };
     static_assert(KDW + 2 < 64, "vmcnt holds 6 bits");
     // All but the newest N vector-memory operations retired (they return in order).
@@ -222,12 +271,10 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
     copy_tile(0, IC<0>{});
     if (has_gate && touch_t < 1) touch_gate();
     if constexpr (R == 3) {
-      if (1 < nkt) {
-        copy_tile(1, IC<1>{});
-        wait_keep(IC<KDW>{});  // the query rows and tile 0 landed; tile 1 may stay in flight
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-      }
+      // Without a tile 1, copies of nothing stand in for it (copy_tile), so that one
+      // wait count holds on every path.
+      copy_tile(1, IC<1>{});
+      wait_keep(IC<KDW>{});  // the query rows and tile 0 landed; tile 1 may stay in flight
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);
     }
@@ -281,21 +328,20 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
     // every slot index is a constant.
     auto interval = [&](int t, auto cur) {
       constexpr int I = decltype(cur)::value, F = (I + R - 1) % R;
-      const bool refill = t + R - 1 < nkt;
       if (has_gate && touch_t >= 1 && t == touch_t) touch_gate();
       // The refill goes into the slot tile t-1 left (every wave's reads of it ended
-      // at the previous barrier). Nothing else of this wave goes to memory in the
-      // loop, so the wait below counts these copies exactly.
-      if (refill) copy_tile(t + R - 1, IC<F>{});
+      // at the previous barrier). Once no tile is left, copies of nothing take its
+      // place, so that every interval issues the same count and one wait holds on every
+      // path. Nothing else of this wave goes to memory in the loop, so the wait below
+      // counts these copies exactly.
+      copy_tile(t + R - 1, IC<F>{});
       stage_a(t, cur);
       // Tile t+1 must have landed before the barrier after which the M-waves read it;
       // the refill just issued (R = 3) may stay in flight.
-      if (t + 1 < nkt) {
-        if (R == 3 && refill)
-          wait_keep(IC<KDW>{});
-        else
-          __builtin_amdgcn_s_waitcnt(0x0F70);
-      }
+      if constexpr (R == 3)
+        wait_keep(IC<KDW>{});
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
       lds_barrier();
     };
     {

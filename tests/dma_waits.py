@@ -37,10 +37,27 @@ flight at key, mixing and prologue key reads) until the next barrier; the query
 and gate rows a wave reads are its own copies, for which its own wait suffices.
 
 Branch correlations are ignored (every path through the graph counts), so the
-check can over-report but not miss a path. The 8-wave variants' helper waves
-refill slots for the product waves; those copies are ordered by the helpers'
-explicit wait and a barrier, which no single wave's counter shows, and are
-outside this check.
+check can over-report but not miss a path.
+
+The 16-row role-split kernel (fused16_kernel, check16) has its similarity waves
+issue every copy and its mixing waves read their rows (transposed key operands,
+gate rows). A copy is visible to another wave only once its issuing wave retired
+it with a vmcnt wait and then passed a barrier the reader passes too; every
+wave runs the same barrier sequence. In a ring of R key slots, tile t's copies
+go out in the interval of tile t-R+1 and both roles read tile t after the
+barrier that ends interval t-1, so at every barrier:
+
+* the first: only the prologue's tile-1 copies (the newest per-tile count of
+  the wave's vector-memory operations) may be in flight; the query rows and
+  tile 0 are read after it;
+* later: a prologue copy (tile 1) may be in flight only at the second (it is
+  read after the third); a loop refill only at the first barrier after its
+  issue with three slots, and at none with two;
+* the last ones (those an s_endpgm follows with no barrier between): nothing,
+  since the mixing waves read the gate rows after them.
+
+The similarity waves' own reads follow from the same rules; the mixing waves
+issue no copy, so their reads see only copies those rules already retired.
 """
 
 import re
@@ -89,7 +106,28 @@ def kernels(asm_text):
     return out
 
 
+def _local_labels(lines):
+    """Give the numeric local labels of inline asm (`1:`, referenced as `1f` / `1b`)
+    unique names and resolve the branches that use them."""
+    out, defs = list(lines), {}
+    for i, t in enumerate(lines):
+        m = re.fullmatch(r'(\d+):', t)
+        if m:
+            out[i] = f'.Lnum{m.group(1)}_{i}:'
+            defs.setdefault(m.group(1), []).append(i)
+    for i, t in enumerate(out):
+        parts = t.split()
+        if len(parts) == 2 and parts[0].startswith(('s_branch', 's_cbranch')):
+            m = re.fullmatch(r'(\d+)([fb])', parts[1])
+            if m:
+                cands = defs[m.group(1)]
+                j = min(c for c in cands if c > i) if m.group(2) == 'f' else max(c for c in cands if c < i)
+                out[i] = f'{parts[0]} .Lnum{m.group(1)}_{j}'
+    return out
+
+
 def _blocks(lines):
+    lines = _local_labels(lines)
     blocks, cur, anon = [], ['entry', []], 0
     for t in lines:
         if t.endswith(':'):
@@ -285,4 +323,154 @@ def check_asm(asm_text):
         bm, nk = int(m.group(1)), int(m.group(2))
         bad, counts = check_kernel(lines, bm, nk)
         out[name] = (bad, counts, (bm, nk))
+    return out
+
+
+_KERNEL16 = re.compile(r'^(_ZN4avey14fused16_kernelI\w+):', re.M)
+_SHAPE16 = re.compile(r'fused16_kernelI\w+?Li(\d+)ELb')
+
+
+def ring16(nk):
+    """(R, copies per similarity wave per key tile) of the 16-row role-split kernel
+    with NK 32-feature steps per slice, as its LDS geometry fixes them (G16)."""
+    cpr = 4 * nk
+    cprp = (cpr + 7) // 8 * 8
+    tile = 4 * 32 * cprp * 16
+    small = 2 * (2 * 2 * 64 * 16) + 2 * 2 * 32 * 4 + 2 * 16 * 4 + 32 * 4 + 256
+    r = 3 if 3 * tile + small <= 160 * 1024 else 2
+    return r, 2 * (cprp // 4)
+
+
+def kernels16(asm_text):
+    out = {}
+    for m in _KERNEL16.finditer(asm_text):
+        name = m.group(1)
+        body = asm_text[m.end():asm_text.index('.Lfunc_end', m.end())]
+        lines = []
+        for raw in body.split('\n'):
+            t = ' '.join(raw.split(';')[0].split())
+            if not t or (t.startswith('.') and not t.startswith('.LBB')):
+                continue
+            lines.append(t)
+        out[name] = lines
+    return out
+
+
+def _dataflow(blocks, succ):
+    """State (copy -> Pareto front of (loads since, barriers since)) before every
+    instruction, keyed (block, position): plain per-wave counting, every path."""
+    state_in = [None] * len(blocks)
+    state_in[0] = {}
+    work = [0]
+    before = {}
+    while work:
+        k = work.pop(0)
+        st = {c: list(f) for c, f in state_in[k].items()}
+        for p, t in enumerate(blocks[k][1]):
+            before[(k, p)] = st
+            m = re.search(r'vmcnt\((\d+)\)', t) if t.startswith('s_waitcnt') else None
+            if m:
+                n = int(m.group(1))
+                st = {c: [q for q in f if q[0] < n] for c, f in st.items()}
+                st = {c: f for c, f in st.items() if f}
+            elif t.startswith('s_barrier'):
+                st = {c: [(q[0], min(q[1] + 1, CAP_BARRIERS)) for q in f] for c, f in st.items()}
+            elif _is_vmem_load(t):
+                st = {c: [(min(q[0] + 1, CAP_LOADS), q[1]) for q in f] for c, f in st.items()}
+                if _is_copy(t) and not _is_touch(t):
+                    st[(k, p)] = [(0, 0)]
+        for s2 in succ[k]:
+            if state_in[s2] is None:
+                state_in[s2] = {c: list(f) for c, f in st.items()}
+                work.append(s2)
+                continue
+            new, changed = {c: list(f) for c, f in state_in[s2].items()}, False
+            for c, f in st.items():
+                front = new.get(c, [])
+                for q in f:
+                    front, ch = _add(front, q)
+                    changed |= ch
+                new[c] = front
+            if changed:
+                state_in[s2] = new
+                work.append(s2)
+    return before
+
+
+def check16(lines, nk):
+    """Violations [(place, rule)] and per-kind counts of one 16-row role-split kernel."""
+    r, kd = ring16(nk)
+    blocks, succ = _blocks(lines)
+    copies = [(k, p) for k, (_, ins) in enumerate(blocks) for p, t in enumerate(ins)
+              if _is_copy(t) and not _is_touch(t)]
+    # The prologue: what the entry reaches before any barrier (each role's code path
+    # has its own), and the barriers that end it.
+    prologue, first_barriers, seen, work = set(), set(), {0}, [0]
+    while work:
+        k = work.pop()
+        for p, t in enumerate(blocks[k][1]):
+            if t.startswith('s_barrier'):
+                first_barriers.add((k, p))
+                break
+            if _is_copy(t) and not _is_touch(t):
+                prologue.add((k, p))
+        else:
+            for s2 in succ[k]:
+                if s2 not in seen:
+                    seen.add(s2)
+                    work.append(s2)
+    before = _dataflow(blocks, succ)
+    # Final barriers: an s_endpgm is reachable from them without another barrier.
+    reach_end = set()
+    changed = True
+    while changed:
+        changed = False
+        for k, (_, ins) in enumerate(blocks):
+            if k in reach_end:
+                continue
+            tail = ins
+            for idx in range(len(ins) - 1, -1, -1):
+                if ins[idx].startswith('s_barrier'):
+                    tail = None
+                    break
+            ends = any(t.startswith('s_endpgm') for t in ins) or any(s2 in reach_end for s2 in succ[k])
+            if tail is not None and ends:
+                reach_end.add(k)
+                changed = True
+    bad, counts = [], defaultdict(int)
+    for (k, p), st in before.items():
+        t = blocks[k][1][p]
+        if not t.startswith('s_barrier'):
+            continue
+        counts['barrier'] += 1
+        rest = blocks[k][1][p + 1:]
+        final = not any(x.startswith('s_barrier') for x in rest) and (
+            any(x.startswith('s_endpgm') for x in rest) or any(s2 in reach_end for s2 in succ[k]))
+        first = (k, p) in first_barriers
+        for c, front in st.items():
+            why = None
+            if final:
+                why = 'copy in flight at a last barrier'
+            elif first:
+                if any(q[0] >= kd for q in front) or r == 2:
+                    why = 'query rows or tile 0 in flight at the first barrier'
+            elif c in prologue:
+                if max(q[1] for q in front) > (1 if r == 3 else 0):
+                    why = 'prologue tile in flight past the barrier before its interval'
+            elif r == 2 or max(q[1] for q in front) > 0:
+                why = 'refill in flight at a barrier after the one that ends its interval'
+            if why:
+                bad.append((f'{blocks[k][0]}+{p}', f'{why}; copy at {blocks[c[0]][0]}+{c[1]}'))
+    counts['copies'] = len(copies)
+    counts['prologue'] = len(prologue)
+    return bad, dict(counts)
+
+
+def check_asm16(asm_text):
+    """{kernel: (violations, counts, NK)} for every 16-row role-split kernel in a file."""
+    out = {}
+    for name, lines in kernels16(asm_text).items():
+        nk = int(_SHAPE16.search(name).group(1))
+        bad, counts = check16(lines, nk)
+        out[name] = (bad, counts, nk)
     return out

@@ -1,9 +1,11 @@
-"""Every LDS read of copied rows in the fused kernel waits for its copy.
+"""Every LDS read of copied rows in the fused kernels waits for its copy.
 
 The fused sources are compiled to gfx950 assembly with the library's own flags
-and checked by tests/dma_waits.py (its docstring states the rules). The first
-tests pin the checker itself on small hand-written instruction sequences, so that
-the check over the real kernels cannot pass by classifying nothing.
+and checked by tests/dma_waits.py (its docstring states the rules): per wave for
+the 32- and 64-row kernels, and across the two roles of the 16-row kernel, whose
+similarity waves copy the rows its mixing waves read. The first tests pin the
+checker itself on small hand-written instruction sequences, so that the check
+over the real kernels cannot pass by classifying nothing.
 """
 
 import os
@@ -101,6 +103,64 @@ def test_query_split_needs_the_wait_before_the_barrier():
     assert not _bad([COPY] * (nq + kdma) + [f's_waitcnt vmcnt({kdma})'] + QUERY, bm, nk)
 
 
+def _bad16(lines, nk=6):
+    bad, _ = dw.check16(lines + ['s_endpgm'], nk)
+    return bad
+
+
+def test_ring16_geometry():
+    # (R, copies per similarity wave per tile): three 48 KB slots at 768 features,
+    # two 64 KB ones at 1024.
+    assert dw.ring16(6) == (3, 12)
+    assert dw.ring16(8) == (2, 16)
+    assert dw.ring16(2) == (3, 4)
+
+
+def test_role_split_cross_wave_rules():
+    r, kd = dw.ring16(6)
+    tile = [COPY] * kd
+    pro = [COPY] * 6 + tile + tile  # query rows, tile 0, tile 1
+    bar = ['s_waitcnt lgkmcnt(0)', 's_barrier']
+    # First barrier: only tile 1 (the newest kd copies) may still be in flight.
+    assert not _bad16(pro + [f's_waitcnt vmcnt({kd})'] + bar + [f's_waitcnt vmcnt(0)'] + bar)
+    assert _bad16(pro + [f's_waitcnt vmcnt({kd + 1})'] + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    # Tile 1 may pass the second barrier but not the third.
+    seq = pro + [f's_waitcnt vmcnt({kd})'] + bar + bar
+    assert not _bad16(seq + tile + [f's_waitcnt vmcnt({kd})'] + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    assert _bad16(seq + tile + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    # A refill may be in flight at the barrier that ends its interval (three slots),
+    # not at the next one.
+    loop = [f's_waitcnt vmcnt(0)'] + bar
+    assert not _bad16(loop + tile + [f's_waitcnt vmcnt({kd})'] + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    assert _bad16(loop + tile + bar + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    # Two slots: no refill may cross a barrier.
+    r8, kd8 = dw.ring16(8)
+    tile8 = [COPY] * kd8
+    assert _bad16([f's_waitcnt vmcnt(0)'] + bar + tile8 + bar + ['s_waitcnt vmcnt(0)'] + bar, nk=8)
+    assert not _bad16([f's_waitcnt vmcnt(0)'] + bar + tile8 + ['s_waitcnt vmcnt(0)'] + bar + bar, nk=8)
+    # The last barrier (the mixing waves read the gate rows after it): nothing in flight.
+    assert _bad16(loop + [COPY] + bar)
+    assert not _bad16(loop + [COPY, 's_waitcnt vmcnt(0)'] + bar)
+    # Touches land in a word no one reads: never counted.
+    assert not _bad16(loop + [TOUCH] + bar)
+    # Every path counts: a wait on one arm of a branch only.
+    br = ['s_cbranch_scc1 .LBB0_9', 's_waitcnt vmcnt(0)', '.LBB0_9:']
+    assert _bad16(loop + [COPY] + br + bar)
+    assert not _bad16(loop + [COPY, 's_waitcnt vmcnt(0)'] + br + bar)
+
+
+def test_copy_or_pad_blocks_count_one_operation_on_either_path():
+    # The inline-asm block issues a copy or a 4-byte pad (numeric local labels): a wait
+    # that keeps the newest kd operations then retires every older copy on every path.
+    r, kd = dw.ring16(6)
+    block = ['s_cmp_eq_u32 s14, 0', 's_cbranch_scc1 1f', COPY, 's_branch 2f', '1:', 's_mov_b32 m0, s7', TOUCH, '2:']
+    bar = ['s_waitcnt lgkmcnt(0)', 's_barrier']
+    old = ['s_waitcnt vmcnt(0)'] + bar + [COPY] * kd
+    assert not _bad16(old + block * kd + [f's_waitcnt vmcnt({kd})'] + bar + ['s_waitcnt vmcnt(0)'] + bar)
+    # One operation short: an older copy survives the wait.
+    assert _bad16(old + block * (kd - 1) + [f's_waitcnt vmcnt({kd})'] + bar + bar + ['s_waitcnt vmcnt(0)'] + bar)
+
+
 def _compile(src, out_dir):
     out = os.path.join(out_dir, os.path.splitext(src)[0] + '.s')
     cmd = [_build.hipcc(), *_build.HIP_FLAGS, *_build.EXTRA_FLAGS.get(src, []), '--cuda-device-only', '-S',
@@ -116,14 +176,21 @@ def test_fused_kernels_wait_for_their_copies(tmp_path):
     sources = [s for s in _build.SOURCES if s.startswith('avey_fused_bm')]
     with ThreadPoolExecutor(max_workers=min(6, os.cpu_count() or 1)) as pool:
         files = list(pool.map(lambda s: _compile(s, str(tmp_path)), sources))
-    checked = 0
+    checked = checked16 = 0
     problems = []
     for path in files:
-        for name, (bad, counts, (bm, nk)) in dw.check_asm(open(path).read()).items():
+        text = open(path).read()
+        for name, (bad, counts, (bm, nk)) in dw.check_asm(text).items():
             checked += 1
             # Non-vacuous: the key, query, mixing and gate reads were all found.
             for role in ('A', 'Q', 'T', 'G'):
                 assert counts.get(role, 0) > 0, (name, counts)
             problems += [(name, b) for b in bad[:3]]
+        # The 16-row role-split kernels: copies of one wave read by another.
+        for name, (bad, counts, nk) in dw.check_asm16(text).items():
+            checked16 += 1
+            assert counts['barrier'] > 0 and counts['prologue'] > 0, (name, counts)
+            problems += [(name, b) for b in bad[:3]]
     assert checked >= 6 * 10, checked
+    assert checked16 >= 4 * 24, checked16
     assert not problems, problems[:6]
