@@ -12,7 +12,9 @@
 //   dz = r * (P^T dnum + J(dS zhat + dS^T zhat)),
 //   J(x) = (x - zhat (zhat . x)) / ||z||  (||z|| >= norm_eps), else x / norm_eps.
 //
-// Kernels (all fp32 arithmetic, fp32 MFMA v_mfma_f32_16x16x4f32):
+// Kernels (arithmetic type A: fp32 with v_mfma_f32_16x16x4f32, or fp64 with
+// v_mfma_f64_16x16x4f64 for the normalised (Avey-B) calls, whose gradients divide by
+// signed row sums that may cancel; a bf16 MFMA variant follows further down):
 //   bwd_prep   row norms ||z|| of the masked rows; clears the dv / dbias accumulators.
 //   bwd_rows   one workgroup per (batch item, 16 query rows). Pass 1 over key
 //              tiles recomputes S, P, num and den (the forward); the epilogue
@@ -42,9 +44,27 @@ constexpr int kRows = 16;      // query (bwd_rows) or key (bwd_cols) rows per wo
 constexpr int kTile = 64;      // rows of the other side per pipeline step
 constexpr int kPitch = kTile + 4;  // LDS row pitch of a [16][64] tile (floats)
 
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+// Same operand layout as the fp32 form (lane (lg, lr) supplies A[lr][lg] and
+// B[lg][lr]), but lane (lg, lr) holds C[lg + 4 i][lr] in result register i.
+__device__ __forceinline__ f64x4 mfma4(double a, double b, f64x4 c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// Row of the 16 x 16 result that lane group lg holds in accumulator element i.
+template <typename A>
+__device__ __forceinline__ int acc_row(int lg, int i) {
+  return sizeof(A) == 8 ? lg + 4 * i : 4 * lg + i;
+}
+
+template <typename A> struct Vec4;
+template <> struct Vec4<float> { using type = f32x4; };
+template <> struct Vec4<double> { using type = f64x4; };
+template <typename A> using v4 = typename Vec4<A>::type;
 
 // Element loads converted to fp32.
 template <typename T> struct Io;
@@ -70,17 +90,22 @@ template <> struct Io<_Float16> {
   }
   __device__ static void put(_Float16* p, float x) { *p = (_Float16)x; }
 };
+// fp64 workspace rows of the fp64 path (dnum); 4-element loads are 32-byte aligned.
+template <> struct Io<double> {
+  __device__ static double one(const double* p) { return *p; }
+  __device__ static f64x4 four(const double* p) { return *(const f64x4*)p; }
+};
 
-// Four consecutive features d..d+3 of one row (zero past D). `vec`: rows are
-// 4-element aligned (D % 4 == 0), so a vector load is in bounds when d + 4 <= D.
-template <typename T>
-__device__ __forceinline__ f32x4 row4(const T* row, int d, int D, bool vec) {
-  if (vec && d + 4 <= D) return Io<T>::four(row + d);
-  f32x4 x = {0.f, 0.f, 0.f, 0.f};
-  if (d < D) x[0] = Io<T>::one(row + d);
-  if (d + 1 < D) x[1] = Io<T>::one(row + d + 1);
-  if (d + 2 < D) x[2] = Io<T>::one(row + d + 2);
-  if (d + 3 < D) x[3] = Io<T>::one(row + d + 3);
+// Four consecutive features d..d+3 of one row (zero past D), converted to A. `vec`:
+// rows are 4-element aligned (D % 4 == 0), so a vector load is in bounds when d + 4 <= D.
+template <typename A, typename T>
+__device__ __forceinline__ v4<A> row4(const T* row, int d, int D, bool vec) {
+  if (vec && d + 4 <= D) return __builtin_convertvector(Io<T>::four(row + d), v4<A>);
+  v4<A> x = {A(0), A(0), A(0), A(0)};
+  if (d < D) x[0] = (A)Io<T>::one(row + d);
+  if (d + 1 < D) x[1] = (A)Io<T>::one(row + d + 1);
+  if (d + 2 < D) x[2] = (A)Io<T>::one(row + d + 2);
+  if (d + 3 < D) x[3] = (A)Io<T>::one(row + d + 3);
   return x;
 }
 
@@ -89,30 +114,30 @@ __device__ __forceinline__ f32x4 row4(const T* row, int d, int D, bool vec) {
 // zeros and is not read. Lane (lg, lr) feeds features 16s + 4lg + t at sub-step
 // t of step s to both operands (any bijection of the contracted index gives the
 // same sum), so every load is four consecutive features. Result: lane holds
-// C[4 lg + i][lr], i = 0..3.
-template <typename TA, typename TB>
-__device__ __forceinline__ f32x4 row_dot(const TA* a, float sa, const TB* b, float sb, int D, bool vec, int lg) {
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+// C[acc_row<A>(lg, i)][lr], i = 0..3.
+template <typename A, typename TA, typename TB>
+__device__ __forceinline__ v4<A> row_dot(const TA* a, A sa, const TB* b, A sb, int D, bool vec, int lg) {
+  v4<A> c = {A(0), A(0), A(0), A(0)};
   const int steps = (D + 15) >> 4;
   for (int s = 0; s < steps; ++s) {
     const int d = 16 * s + 4 * lg;
-    f32x4 x = a ? row4<TA>(a, d, D, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 y = b ? row4<TB>(b, d, D, vec) : f32x4{0.f, 0.f, 0.f, 0.f};
+    v4<A> x = a ? row4<A, TA>(a, d, D, vec) : v4<A>{A(0), A(0), A(0), A(0)};
+    v4<A> y = b ? row4<A, TB>(b, d, D, vec) : v4<A>{A(0), A(0), A(0), A(0)};
 #pragma unroll
     for (int t = 0; t < 4; ++t) c = mfma4(x[t] * sa, y[t] * sb, c);
   }
   return c;
 }
 
-// acc[t] (16 x 16, columns 16 (w + 4t) ..) += A (16 x 64, LDS, pitch kPitch)
+// acc[t] (16 x 16, columns 16 (w + 4t) ..) += At (16 x 64, LDS, pitch kPitch)
 // times rows r0 .. r0+63 of Y (row stride D). Row r0 + 4s + lg is read only when
 // bit s of `rows_ok` is set.
-template <typename T, int MAXT>
-__device__ __forceinline__ void rows_acc(f32x4 (&acc)[MAXT], const float* A, const T* Y, int64_t r0, uint32_t rows_ok,
+template <typename A, typename T, int MAXT>
+__device__ __forceinline__ void rows_acc(v4<A> (&acc)[MAXT], const A* At, const T* Y, int64_t r0, uint32_t rows_ok,
                                          int D, int w, int lr, int lg) {
-  float af[16];
+  A af[16];
 #pragma unroll
-  for (int s = 0; s < 16; ++s) af[s] = A[lr * kPitch + 4 * s + lg];
+  for (int s = 0; s < 16; ++s) af[s] = At[lr * kPitch + 4 * s + lg];
   const int ntiles = (D + 15) >> 4;
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
@@ -120,10 +145,10 @@ __device__ __forceinline__ void rows_acc(f32x4 (&acc)[MAXT], const float* A, con
     if (tile >= ntiles) break;
     const int col = 16 * tile + lr;
     const T* y = Y + (r0 + lg) * (int64_t)D + col;
-    float yv[16];
+    A yv[16];
 #pragma unroll
     for (int s = 0; s < 16; ++s)
-      yv[s] = (((rows_ok >> s) & 1u) && col < D) ? Io<T>::one(y + (int64_t)(4 * s) * D) : 0.f;
+      yv[s] = (((rows_ok >> s) & 1u) && col < D) ? (A)Io<T>::one(y + (int64_t)(4 * s) * D) : A(0);
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc[t] = mfma4(af[s], yv[s], acc[t]);
   }
@@ -136,9 +161,13 @@ __device__ __forceinline__ bool row_valid(const uint8_t* valid, int64_t b, int64
 __device__ __forceinline__ float inv_norm(const float* nrm, int64_t idx, float norm_eps) {
   return 1.f / fmaxf(nrm[idx], norm_eps);
 }
+__device__ __forceinline__ double inv_norm(const double* nrm, int64_t idx, double norm_eps) {
+  return 1.0 / fmax(nrm[idx], norm_eps);
+}
 
 // Sum over the 16 lanes of a lane group (lanes sharing lg).
-__device__ __forceinline__ float sum16(float x) {
+template <typename A>
+__device__ __forceinline__ A sum16(A x) {
   x += __shfl_xor(x, 1);
   x += __shfl_xor(x, 2);
   x += __shfl_xor(x, 4);
@@ -147,21 +176,22 @@ __device__ __forceinline__ float sum16(float x) {
 }
 
 // d act(u) / du; the derivatives autograd takes of ops.py:49-58.
-__device__ __forceinline__ float act_grad(float x, int act) {
+template <typename A>
+__device__ __forceinline__ A act_grad(A x, int act) {
   switch (act) {
-    case AVEY_ACT_RELU: return x > 0.f ? 1.f : 0.f;
-    case AVEY_ACT_RELU2: return x > 0.f ? 2.f * x : 0.f;
+    case AVEY_ACT_RELU: return x > A(0) ? A(1) : A(0);
+    case AVEY_ACT_RELU2: return x > A(0) ? A(2) * x : A(0);
     case AVEY_ACT_SILU: {
-      float e = expf(-fabsf(x));
-      float s = x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
-      return s * (1.f + x * (1.f - s));
+      A e = exp(-fabs(x));
+      A s = x >= A(0) ? A(1) / (A(1) + e) : e / (A(1) + e);
+      return s * (A(1) + x * (A(1) - s));
     }
     case AVEY_ACT_GELU: {
-      const float k = 0.7978845608028654f;
-      float t = tanhf(k * (x + 0.044715f * x * x * x));
-      return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * k * (1.f + 3.f * 0.044715f * x * x);
+      const A k = A(0.7978845608028654);
+      A t = tanh(k * (x + A(0.044715) * x * x * x));
+      return A(0.5) * (A(1) + t) + A(0.5) * x * (A(1) - t * t) * k * (A(1) + A(3) * A(0.044715) * x * x);
     }
-    default: return 1.f;
+    default: return A(1);
   }
 }
 
@@ -183,22 +213,26 @@ __device__ __forceinline__ void tile_of_block(int64_t B, int64_t nt, bool heavy_
   if (heavy_last) t = nt - 1 - t;
 }
 
-struct Ws {
-  float *nrm, *dnum, *dden, *dzr, *dv, *db;
+// Workspace of a path computing in A (the bf16 path: A = float).
+template <typename A>
+struct WsT {
+  A *nrm, *dnum, *dden, *dzr, *dv, *db;
   // bf16 path only: z transposed per batch item [D][cp] (padded rows zero),
   // dnum in bf16 row-major [C][D] and transposed [D][cp].
   __bf16 *zt, *dn16, *dnt;
   int64_t cp;
 };
+using Ws = WsT<float>;
 
-// Workspace layout (each part 256-byte aligned): nrm [B*C], dden [B*C], dzr
-// [B*C*D] fp32; then the fp32 path's dnum [B*C*D] fp32, or the bf16 path's zt
-// [B*D*cp], dn16 [B*C*D] and dnt [B*D*cp] bf16 (cp = C rounded up to 128); then
-// dv [C*C] and dbias [D] fp32 when present.
+// Workspace layout in elements of A (each part 64 elements, so at least 256 bytes,
+// aligned): nrm [B*C], dden [B*C], dzr [B*C*D]; then the A paths' dnum [B*C*D], or
+// the bf16 path's zt [B*D*cp], dn16 [B*C*D] and dnt [B*D*cp] bf16 (cp = C rounded up
+// to 128); then dv [C*C] and dbias [D] when present.
 __host__ __device__ inline int64_t up64(int64_t n) { return (n + 63) & ~int64_t(63); }
 
-__host__ inline int64_t ws_floats_parts(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast,
-                                        Ws* w, void* base) {
+template <typename A>
+__host__ inline int64_t ws_parts(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast,
+                                 WsT<A>* w, void* base) {
   const int64_t cp = (C + 127) & ~int64_t(127);  // a multiple of the bf16 kernels' 128-row tiles
   int64_t off = 0;
   auto take = [&](int64_t n) { const int64_t o = off; off += up64(n); return o; };
@@ -210,7 +244,7 @@ __host__ inline int64_t ws_floats_parts(int64_t B, int64_t C, int64_t D, bool ha
   const int64_t o_dv = has_v ? take(C * C) : -1;
   const int64_t o_db = has_bias ? take(D) : -1;
   if (w) {
-    float* f = (float*)base;
+    A* f = (A*)base;
     w->nrm = f + o_nrm;
     w->dden = f + o_dden;
     w->dzr = f + o_dzr;
@@ -225,50 +259,47 @@ __host__ inline int64_t ws_floats_parts(int64_t B, int64_t C, int64_t D, bool ha
   return off;
 }
 
-__host__ inline Ws carve(void* base, int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
-  Ws w;
-  ws_floats_parts(B, C, D, has_v, has_bias, fast, &w, base);
+template <typename A>
+__host__ inline WsT<A> carve(void* base, int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
+  WsT<A> w;
+  ws_parts<A>(B, C, D, has_v, has_bias, fast, &w, base);
   return w;
-}
-
-__host__ inline int64_t ws_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
-  return ws_floats_parts(B, C, D, has_v, has_bias, fast, nullptr, nullptr);
 }
 
 // One wave per row: ||z|| of the masked row. Every thread also clears a share of
 // the dv / dbias accumulators.
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p, Ws ws) {
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(BwdParams p, WsT<A> ws) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t rows = p.B * p.C;
   if (row < rows) {
     const int64_t b = row / p.C, c = row % p.C;
-    float ss = 0.f;
+    A ss = A(0);
     if (row_valid(p.valid, b, p.C, c)) {
       const T* z = (const T*)p.z + row * p.D;
       for (int64_t d = lane; d < p.D; d += 64) {
-        float x = Io<T>::one(z + d);
+        A x = (A)Io<T>::one(z + d);
         ss += x * x;
       }
     }
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if (lane == 0) ws.nrm[row] = sqrtf(ss);
+    if (lane == 0) ws.nrm[row] = sqrt(ss);
   }
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (int64_t)gridDim.x * blockDim.x;
   if (ws.dv)
-    for (int64_t i = tid; i < p.C * p.C; i += nt) ws.dv[i] = 0.f;
+    for (int64_t i = tid; i < p.C * p.C; i += nt) ws.dv[i] = A(0);
   if (ws.db)
-    for (int64_t i = tid; i < p.D; i += nt) ws.db[i] = 0.f;
+    for (int64_t i = tid; i < p.D; i += nt) ws.db[i] = A(0);
 }
 
-template <typename T, int MAXT>
-__global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
+template <typename T, typename A, int MAXT>
+__global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
   constexpr int dp = 64 * MAXT + 4;          // pitch of dnl; D <= 64 * MAXT
-  __shared__ float tile[kRows * kPitch];     // [16][kPitch]: P, then dS * inv(key)
-  __shared__ float red[4 * kRows];           // [4 waves][16]
-  __shared__ float stat[2 * kRows];          // den, dden of the block's rows
-  __shared__ __attribute__((aligned(16))) float dnl[kRows * dp];  // dnum of the block's rows
+  __shared__ A tile[kRows * kPitch];         // [16][kPitch]: P, then dS * inv(key)
+  __shared__ A red[4 * kRows];               // [4 waves][16]
+  __shared__ A stat[2 * kRows];              // den, dden of the block's rows
+  __shared__ __attribute__((aligned(32))) A dnl[kRows * dp];  // dnum of the block's rows
   const int D = (int)p.D;
   // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
   const int64_t C = p.C;
@@ -278,7 +309,7 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const bool vec = (D & 3) == 0;
-  const float neps = (float)p.norm_eps;
+  const A neps = (A)p.norm_eps;
   const T* zb = (const T*)p.z + b * C * D;
   const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
   const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
@@ -288,49 +319,49 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
   const int64_t qa = q0 + lr;
   const bool qa_ok = row_valid(p.valid, b, C, qa);
   const T* qa_row = qa_ok ? zb + qa * D : nullptr;
-  const float qa_inv = qa_ok ? inv_norm(ws.nrm, b * C + qa, neps) : 0.f;
+  const A qa_inv = qa_ok ? inv_norm(ws.nrm, b * C + qa, neps) : A(0);
 
   // ---- pass 1: num, den ----
-  f32x4 acc[MAXT];
+  v4<A> acc[MAXT];
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float den4[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MAXT; ++t) acc[t] = v4<A>{A(0), A(0), A(0), A(0)};
+  A den4[4] = {A(0), A(0), A(0), A(0)};
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * kTile + 16 * w + lr;  // this lane's key (B row, output column)
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
-    f32x4 s4 = row_dot<T, T>(qa_row, qa_inv, k_ok ? zb + k * D : nullptr, k_inv, D, vec, lg);
+    const A k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : A(0);
+    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_inv, k_ok ? zb + k * D : nullptr, k_inv, D, vec, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t q = q0 + 4 * lg + i;
+      const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      float pv = 0.f;
-      if (m) pv = s4[i] * (vt ? Io<T>::one(vt + q * C + k) : 1.f);
+      A pv = A(0);
+      if (m) pv = s4[i] * (vt ? (A)Io<T>::one(vt + q * C + k) : A(1));
       den4[i] += pv;
-      tile[(4 * lg + i) * kPitch + 16 * w + lr] = pv;
+      tile[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = pv;
     }
     uint32_t rows_ok = 0;
 #pragma unroll
     for (int s = 0; s < 16; ++s) rows_ok |= (uint32_t)row_valid(p.valid, b, C, kt * kTile + 4 * s + lg) << s;
     __syncthreads();
-    rows_acc<T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
+    rows_acc<A, T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
     __syncthreads();
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float x = sum16(den4[i]);
-    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+    A x = sum16(den4[i]);
+    if (lr == 0) red[w * kRows + acc_row<A>(lg, i)] = x;
   }
   __syncthreads();
   if (threadIdx.x < kRows) {
     const int i = threadIdx.x;
-    stat[i] = red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i] + (float)p.eps;
+    stat[i] = red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i] + (A)p.eps;
   }
   __syncthreads();
 
   // ---- epilogue 1: dz_tl, dnum, dden, dbias ----
   const int ntiles = (D + 15) >> 4;
-  float ddp[4] = {0.f, 0.f, 0.f, 0.f};
+  A ddp[4] = {A(0), A(0), A(0), A(0)};
   const T* gb = p.gate ? (const T*)p.gate + b * C * D : nullptr;
   const T* ob = (const T*)p.dout + b * C * D;
   T* dgb = p.dgate ? (T*)p.dgate + b * C * D : nullptr;
@@ -339,21 +370,21 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
     const int tile_i = w + 4 * t;
     if (tile_i >= ntiles) break;
     const int col = 16 * tile_i + lr;
-    float dbs = 0.f;
+    A dbs = A(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = 4 * lg + i;
+      const int row = acc_row<A>(lg, i);
       const int64_t q = q0 + row;
-      float dn = 0.f;
+      A dn = A(0);
       if (col < D && q < C) {
         const bool rq = row_valid(p.valid, b, C, q);
-        const float den = stat[row];
-        const float y = p.normalize ? acc[t][i] / den : acc[t][i];
-        const float u = y + (p.bias ? Io<T>::one((const T*)p.bias + col) : 0.f);
-        const float go = rq ? Io<T>::one(ob + q * D + col) : 0.f;
-        const float gt = gb ? (rq ? Io<T>::one(gb + q * D + col) : 0.f) : 1.f;
-        if (dgb) Io<T>::put(dgb + q * D + col, go * activate<float>(u, p.act));
-        const float du = go * gt * act_grad(u, p.act);
+        const A den = stat[row];
+        const A y = p.normalize ? acc[t][i] / den : acc[t][i];
+        const A u = y + (p.bias ? (A)Io<T>::one((const T*)p.bias + col) : A(0));
+        const A go = rq ? (A)Io<T>::one(ob + q * D + col) : A(0);
+        const A gt = gb ? (rq ? (A)Io<T>::one(gb + q * D + col) : A(0)) : A(1);
+        if (dgb) Io<T>::put(dgb + q * D + col, (float)(go * activate<A>(u, p.act)));
+        const A du = go * gt * act_grad(u, p.act);
         dbs += du;
         dn = p.normalize ? du / den : du;
         ddp[i] += du * y;
@@ -369,14 +400,14 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float x = sum16(ddp[i]);
-    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+    A x = sum16(ddp[i]);
+    if (lr == 0) red[w * kRows + acc_row<A>(lg, i)] = x;
   }
   __syncthreads();
   if (threadIdx.x < kRows) {
     const int i = threadIdx.x;
     const int64_t q = q0 + i;
-    float dd = 0.f;
+    A dd = A(0);
     if (p.normalize) dd = -(red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / stat[i];
     stat[kRows + i] = dd;
     if (q < C) ws.dden[b * C + q] = dd;
@@ -385,33 +416,33 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
 
   // ---- pass 2: dP, dS, dv, dS zhat ----
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float* dn_row = dnl + lr * dp;  // A rows of dP = dnum z^T (zeros for rows past C)
+  for (int t = 0; t < MAXT; ++t) acc[t] = v4<A>{A(0), A(0), A(0), A(0)};
+  const A* dn_row = dnl + lr * dp;  // A rows of dP = dnum z^T (zeros for rows past C)
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * kTile + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    const A k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : A(0);
     const T* k_row = k_ok ? zb + k * D : nullptr;
-    f32x4 s4 = row_dot<T, T>(qa_row, qa_inv, k_row, k_inv, D, vec, lg);
-    f32x4 d4 = row_dot<float, T>(dn_row, 1.f, k_row, 1.f, D, vec, lg);
+    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_inv, k_row, k_inv, D, vec, lg);
+    v4<A> d4 = row_dot<A, A, T>(dn_row, A(1), k_row, A(1), D, vec, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t q = q0 + 4 * lg + i;
+      const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      float dsv = 0.f;
+      A dsv = A(0);
       if (m) {
-        const float dpv = d4[i] + stat[kRows + 4 * lg + i];
-        const float vv = vt ? Io<T>::one(vt + q * C + k) : 1.f;
+        const A dpv = d4[i] + stat[kRows + acc_row<A>(lg, i)];
+        const A vv = vt ? (A)Io<T>::one(vt + q * C + k) : A(1);
         dsv = dpv * vv * k_inv;
         if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i]);
       }
-      tile[(4 * lg + i) * kPitch + 16 * w + lr] = dsv;
+      tile[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = dsv;
     }
     uint32_t rows_ok = 0;
 #pragma unroll
     for (int s = 0; s < 16; ++s) rows_ok |= (uint32_t)row_valid(p.valid, b, C, kt * kTile + 4 * s + lg) << s;
     __syncthreads();
-    rows_acc<T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
+    rows_acc<A, T, MAXT>(acc, tile, zb, kt * kTile, rows_ok, D, w, lr, lg);
     __syncthreads();
   }
 #pragma unroll
@@ -421,18 +452,18 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, Ws ws) {
     const int col = 16 * tile_i + lr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t q = q0 + 4 * lg + i;
+      const int64_t q = q0 + acc_row<A>(lg, i);
       if (col < D && q < C) ws.dzr[(b * C + q) * D + col] = acc[t][i];
     }
   }
 }
 
-template <typename T, int MAXT>
-__global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
-  __shared__ float pt[kRows * kPitch];  // P^T tile [16 keys][64 queries]
-  __shared__ float dt[kRows * kPitch];  // (dS * inv(query))^T tile
-  __shared__ float red[4 * kRows];
-  __shared__ float rad[kRows];
+template <typename T, typename A, int MAXT>
+__global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
+  __shared__ A pt[kRows * kPitch];  // P^T tile [16 keys][64 queries]
+  __shared__ A dt[kRows * kPitch];  // (dS * inv(query))^T tile
+  __shared__ A red[4 * kRows];
+  __shared__ A rad[kRows];
   const int D = (int)p.D;
   const int64_t C = p.C;
   int64_t b, ktile;
@@ -441,40 +472,40 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const bool vec = (D & 3) == 0;
-  const float neps = (float)p.norm_eps;
+  const A neps = (A)p.norm_eps;
   const T* zb = (const T*)p.z + b * C * D;
-  const float* dnb = ws.dnum + b * C * D;
+  const A* dnb = ws.dnum + b * C * D;
   const T* vt = (const T*)p.v;
 
   const int64_t ka = k0 + lr;  // A row of the row dots: key k0 + lr
   const bool ka_ok = row_valid(p.valid, b, C, ka);
   const T* ka_row = ka_ok ? zb + ka * D : nullptr;
-  const float ka_inv = ka_ok ? inv_norm(ws.nrm, b * C + ka, neps) : 0.f;
+  const A ka_inv = ka_ok ? inv_norm(ws.nrm, b * C + ka, neps) : A(0);
 
-  f32x4 acc1[MAXT], acc2[MAXT];
+  v4<A> acc1[MAXT], acc2[MAXT];
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MAXT; ++t) acc1[t] = acc2[t] = v4<A>{A(0), A(0), A(0), A(0)};
   const int64_t qstart = p.causal ? k0 : 0;
   for (int64_t qt = qstart; qt < C; qt += kTile) {
     const int64_t q = qt + 16 * w + lr;  // this lane's query (B row, output column)
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
-    const float q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
-    f32x4 s4 = row_dot<T, T>(ka_row, ka_inv, q_ok ? zb + q * D : nullptr, q_inv, D, vec, lg);
-    f32x4 d4 = row_dot<T, float>(ka_row, 1.f, q_in ? dnb + q * D : nullptr, 1.f, D, vec, lg);
-    const float dd = q_in ? ws.dden[b * C + q] : 0.f;
+    const A q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : A(0);
+    v4<A> s4 = row_dot<A, T, T>(ka_row, ka_inv, q_ok ? zb + q * D : nullptr, q_inv, D, vec, lg);
+    v4<A> d4 = row_dot<A, T, A>(ka_row, A(1), q_in ? dnb + q * D : nullptr, A(1), D, vec, lg);
+    const A dd = q_in ? ws.dden[b * C + q] : A(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + 4 * lg + i;
+      const int64_t k = k0 + acc_row<A>(lg, i);
       const bool m = q_in && row_valid(p.valid, b, C, k) && (!p.causal || k <= q);
-      float pv = 0.f, dsv = 0.f;
+      A pv = A(0), dsv = A(0);
       if (m) {
-        const float vv = vt ? Io<T>::one(vt + q * C + k) : 1.f;
+        const A vv = vt ? (A)Io<T>::one(vt + q * C + k) : A(1);
         pv = s4[i] * vv;
         dsv = (d4[i] + dd) * vv * q_inv;
       }
-      pt[(4 * lg + i) * kPitch + 16 * w + lr] = pv;
-      dt[(4 * lg + i) * kPitch + 16 * w + lr] = dsv;
+      pt[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = pv;
+      dt[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = dsv;
     }
     uint32_t in_ok = 0, rows_ok = 0;
 #pragma unroll
@@ -484,14 +515,14 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
       rows_ok |= (uint32_t)row_valid(p.valid, b, C, r) << s;
     }
     __syncthreads();
-    rows_acc<float, MAXT>(acc1, pt, dnb, qt, in_ok, D, w, lr, lg);
-    rows_acc<T, MAXT>(acc2, dt, zb, qt, rows_ok, D, w, lr, lg);
+    rows_acc<A, A, MAXT>(acc1, pt, dnb, qt, in_ok, D, w, lr, lg);
+    rows_acc<A, T, MAXT>(acc2, dt, zb, qt, rows_ok, D, w, lr, lg);
     __syncthreads();
   }
 
   // Epilogue: dzhat = key-side + query-side parts; J; row mask.
   const int ntiles = (D + 15) >> 4;
-  float rp[4] = {0.f, 0.f, 0.f, 0.f};
+  A rp[4] = {A(0), A(0), A(0), A(0)};
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     const int tile_i = w + 4 * t;
@@ -499,26 +530,26 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
     const int col = 16 * tile_i + lr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + 4 * lg + i;
+      const int64_t k = k0 + acc_row<A>(lg, i);
       if (col < D && row_valid(p.valid, b, C, k)) {
-        const float g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
+        const A g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
         acc2[t][i] = g;
-        rp[i] += Io<T>::one(zb + k * D + col) * g;
+        rp[i] += (A)Io<T>::one(zb + k * D + col) * g;
       }
     }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float x = sum16(rp[i]);
-    if (lr == 0) red[w * kRows + 4 * lg + i] = x;
+    A x = sum16(rp[i]);
+    if (lr == 0) red[w * kRows + acc_row<A>(lg, i)] = x;
   }
   __syncthreads();
   if (threadIdx.x < kRows) {
     const int i = threadIdx.x;
     const int64_t k = k0 + i;
-    float r = 0.f;
+    A r = A(0);
     if (row_valid(p.valid, b, C, k)) {
-      const float n = ws.nrm[b * C + k];
+      const A n = ws.nrm[b * C + k];
       // zhat . dzhat / ||z|| when the norm is not clamped; no radial term otherwise.
       if (n >= neps) r = (red[i] + red[kRows + i] + red[2 * kRows + i] + red[3 * kRows + i]) / n;
     }
@@ -533,26 +564,26 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, Ws ws) {
     const int col = 16 * tile_i + lr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + 4 * lg + i;
+      const int64_t k = k0 + acc_row<A>(lg, i);
       if (col >= D || k >= C) continue;
-      float g = 0.f;
+      A g = A(0);
       if (row_valid(p.valid, b, C, k)) {
-        const float inv = inv_norm(ws.nrm, b * C + k, neps);
-        const float zh = Io<T>::one(zb + k * D + col) * inv;
-        g = acc1[t][i] + (acc2[t][i] - zh * rad[4 * lg + i]) * inv;
+        const A inv = inv_norm(ws.nrm, b * C + k, neps);
+        const A zh = (A)Io<T>::one(zb + k * D + col) * inv;
+        g = acc1[t][i] + (acc2[t][i] - zh * rad[acc_row<A>(lg, i)]) * inv;
       }
-      Io<T>::put(dzb + k * D + col, g);
+      Io<T>::put(dzb + k * D + col, (float)g);
     }
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, Ws ws) {
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, WsT<A> ws) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (int64_t)gridDim.x * blockDim.x;
   if (p.dv)
-    for (int64_t i = tid; i < p.C * p.C; i += nt) Io<T>::put((T*)p.dv + i, ws.dv[i]);
+    for (int64_t i = tid; i < p.C * p.C; i += nt) Io<T>::put((T*)p.dv + i, (float)ws.dv[i]);
   if (p.dbias)
-    for (int64_t i = tid; i < p.D; i += nt) Io<T>::put((T*)p.dbias + i, ws.db[i]);
+    for (int64_t i = tid; i < p.D; i += nt) Io<T>::put((T*)p.dbias + i, (float)ws.db[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -561,9 +592,10 @@ __global__ __launch_bounds__(256) void bwd_final_kernel(BwdParams p, Ws ws) {
 // similarity is scaled by both inverse norms afterwards, so no operand is
 // re-rounded); products over rows take their right operand from transposed
 // copies (z^T, dnum^T) so that 8 consecutive rows of one column are adjacent.
-// dnum, P and dS are rounded to bf16 as MFMA operands; den, dden, dv, the
-// accumulators and the epilogues stay fp32. Needs D % 8 == 0 and a 16-byte
-// aligned z_tr.
+// P and dS are rounded to bf16 as MFMA operands, and so is dnum in the products
+// over rows (P^T dnum); the row dots of dP take dnum as two bf16 parts (hi and the
+// rounding remainder). den, dden, dv, the accumulators and the epilogues stay fp32.
+// Needs D % 8 == 0 and a 16-byte aligned z_tr.
 
 // The bf16 kernels run NW waves per workgroup: row tiles of KT = 16 NW rows on the
 // other side, a [16][KT] P / dS tile in LDS (pitch KT + 8 bf16), and wave w owning
@@ -641,6 +673,34 @@ __device__ __forceinline__ void row_dot16x2(const __bf16* a1, const __bf16* a2, 
         c1 = mfma16(x1[u], y1[u], c1);
         c2 = mfma16(x2[u], y1[u], c2);
       }
+    }
+  }
+}
+
+// Three row dots sharing the right operand: c1 = a1 b^T, c2 = a2 b^T, c3 = a3 b^T (b
+// loaded once). Same lane layout as row_dot16; a null row is zero and not read.
+__device__ __forceinline__ void row_dot16x3(const __bf16* a1, const __bf16* a2, const __bf16* a3, const __bf16* b,
+                                            int D, int lg, f32x4& c1, f32x4& c2, f32x4& c3) {
+  c1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  c2 = f32x4{0.f, 0.f, 0.f, 0.f};
+  c3 = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int steps = (D + 31) >> 5;
+  for (int s0 = 0; s0 < steps; s0 += 4) {
+    bf16x8 x1[4], x2[4], x3[4], y[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = 32 * (s0 + u) + 8 * lg;
+      const bool in = s0 + u < steps && d < D;
+      x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
+      x2[u] = (a2 && in) ? ld8(a2 + d) : zero8();
+      x3[u] = (a3 && in) ? ld8(a3 + d) : zero8();
+      y[u] = (b && in) ? ld8(b + d) : zero8();
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      c1 = mfma16(x1[u], y[u], c1);
+      c2 = mfma16(x2[u], y[u], c2);
+      c3 = mfma16(x3[u], y[u], c3);
     }
   }
 }
@@ -729,6 +789,11 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
   __shared__ float red[NW * kRows];
   __shared__ float stat[2 * kRows];
   __shared__ __attribute__((aligned(16))) __bf16 dnl[kRows * dp];
+  // dnum - bf16(dnum): with dnl, the row dots of dP see dnum to about 2^-17 of itself,
+  // so dP keeps the exact cancellation between its terms (sum_j P_ij dP_ij = 0 for
+  // the normalised rows) that rounding dnum to bf16 alone would break, and dv and dS
+  // are as accurate as the fp32 products of the reference's autograd.
+  __shared__ __attribute__((aligned(16))) __bf16 dnlo[kRows * dp];
   __shared__ __attribute__((aligned(16))) __bf16 qzl[kRows * dp];  // the block's query rows
   const int D = (int)p.D;
   // Heaviest query tiles first (in causal mode the last ones visit the most key tiles).
@@ -825,6 +890,7 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
       }
       dn4[i] = (__bf16)dn;
       dnl[row * dp + col] = dn4[i];
+      dnlo[row * dp + col] = (__bf16)(dn - (float)dn4[i]);
     }
     if (col < D) *(bf16x4*)(ws.dnt + (b * D + col) * cp + q0 + 4 * lg) = dn4;
     if (ws.db) {
@@ -853,13 +919,15 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   const __bf16* dn_row = dnl + lr * dp;
+  const __bf16* dnlo_row = dnlo + lr * dp;
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
     const __bf16* k_row = k_ok ? zb + k * D : nullptr;
-    f32x4 s4, d4;
-    row_dot16x2<false>(qa_row, dn_row, k_row, nullptr, D, lg, s4, d4);
+    f32x4 s4, d4, d4lo;
+    row_dot16x3(qa_row, dn_row, dnlo_row, k_row, D, lg, s4, d4, d4lo);
+    d4 += d4lo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
@@ -1014,9 +1082,9 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
 
 template <int NW, int MAXT>
 hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
-  Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, true);
+  Ws ws = carve<float>(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, true);
   const int64_t rows = p.B * p.C;
-  hipLaunchKernelGGL(bwd_prep_kernel<__bf16>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd_prep_kernel<__bf16, float>), dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
   hipLaunchKernelGGL(bwd16_transpose_kernel, dim3((unsigned)(ws.cp / 64), (unsigned)cdiv(p.D, 64), (unsigned)p.B),
                      dim3(256), 0, s, p, ws);
   const dim3 grid((unsigned)(cdiv(p.C, kRows) * p.B));  // 1-D, mapped by tile_of_block
@@ -1025,34 +1093,40 @@ hipError_t launch_bwd16_t(const BwdParams& p, hipStream_t s) {
   if (p.dv || p.dbias) {
     const int64_t n = p.dv ? p.C * p.C : p.D;
     const int64_t blocks = cdiv(n, 256) < 1024 ? cdiv(n, 256) : 1024;
-    hipLaunchKernelGGL(bwd_final_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
+    hipLaunchKernelGGL((bwd_final_kernel<__bf16, float>), dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
   }
   return hipGetLastError();
 }
 
-template <typename T, int MAXT>
+template <typename T, typename A, int MAXT>
 hipError_t launch_bwd_t(const BwdParams& p, hipStream_t s) {
-  Ws ws = carve(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, false);
+  WsT<A> ws = carve<A>(p.work, p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr, false);
   const int64_t rows = p.B * p.C;
-  hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd_prep_kernel<T, A>), dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, s, p, ws);
   const dim3 grid((unsigned)(cdiv(p.C, kRows) * p.B));  // 1-D, mapped by tile_of_block
-  hipLaunchKernelGGL((bwd_rows_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
-  hipLaunchKernelGGL((bwd_cols_kernel<T, MAXT>), grid, dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd_rows_kernel<T, A, MAXT>), grid, dim3(256), 0, s, p, ws);
+  hipLaunchKernelGGL((bwd_cols_kernel<T, A, MAXT>), grid, dim3(256), 0, s, p, ws);
   if (p.dv || p.dbias) {
     const int64_t n = p.dv ? p.C * p.C : p.D;
     const int64_t blocks = cdiv(n, 256) < 1024 ? cdiv(n, 256) : 1024;
-    hipLaunchKernelGGL(bwd_final_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
+    hipLaunchKernelGGL((bwd_final_kernel<T, A>), dim3((unsigned)blocks), dim3(256), 0, s, p, ws);
   }
   return hipGetLastError();
 }
 
-template <typename T>
+// Accumulator tiles per wave: 4 waves share the (D + 15) / 16 column tiles. The fp64
+// path adds a 12-tile step so that D = 768 keeps 2 x 12 (not 2 x 16) fp64
+// accumulators of 8 registers each in the cols kernel.
+template <typename T, typename A>
 hipError_t launch_bwd_d(const BwdParams& p, hipStream_t s) {
   const int64_t tiles = cdiv(p.D, 16);
-  if (tiles <= 8) return launch_bwd_t<T, 2>(p, s);
-  if (tiles <= 16) return launch_bwd_t<T, 4>(p, s);
-  if (tiles <= 32) return launch_bwd_t<T, 8>(p, s);
-  return launch_bwd_t<T, 16>(p, s);
+  if (tiles <= 8) return launch_bwd_t<T, A, 2>(p, s);
+  if (tiles <= 16) return launch_bwd_t<T, A, 4>(p, s);
+  if (tiles <= 32) return launch_bwd_t<T, A, 8>(p, s);
+  if constexpr (sizeof(A) == 8) {
+    if (tiles <= 48) return launch_bwd_t<T, A, 12>(p, s);
+  }
+  return launch_bwd_t<T, A, 16>(p, s);
 }
 
 // 8 waves per workgroup: each holds 16-column tiles of up to 8 x 16 features per
@@ -1066,21 +1140,40 @@ hipError_t launch_bwd16(const BwdParams& p, hipStream_t s) {
 
 }  // namespace
 
-bool bwd_fast_path(int dtype, int64_t D, const void* z) {
-  return dtype == AVEY_DTYPE_BF16 && D % 8 == 0 && ((uintptr_t)z & 15) == 0;
+// Normalised (Avey-B) calls compute in fp64 whatever the stored type: their
+// gradients divide by the signed row sums den_i, so an evaluation error e in den_i,
+// S or num moves every gradient that depends on row i by about e * sum|P_i.| / |den_i|.
+// On N(0, 1) inputs that factor reaches 1e4-3e5 (C3, C5): fp32 arithmetic, the
+// reference's own autograd included, then misses the flat tol * (1 + |w|) bound by up
+// to ~900x, and the bf16 operands of the fast path by more; fp64 leaves ~1e-11.
+// The other calls: bf16 with D % 8 == 0 and a 16-byte aligned z_tr take the bf16
+// MFMA path, the rest fp32.
+BwdPath bwd_path(int dtype, int64_t D, const void* z, bool normalize) {
+  if (normalize) return BwdPath::Fp64;
+  if (dtype == AVEY_DTYPE_BF16 && D % 8 == 0 && ((uintptr_t)z & 15) == 0) return BwdPath::Bf16;
+  return BwdPath::Fp32;
 }
 
-int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast) {
-  return ws_floats(B, C, D, has_v, has_bias, fast);
+int64_t bwd_workspace_bytes(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, BwdPath path) {
+  if (path == BwdPath::Fp64) return 8 * ws_parts<double>(B, C, D, has_v, has_bias, false, nullptr, nullptr);
+  return 4 * ws_parts<float>(B, C, D, has_v, has_bias, path == BwdPath::Bf16, nullptr, nullptr);
+}
+
+template <typename A>
+hipError_t launch_bwd_a(const BwdParams& p, int dtype, hipStream_t s) {
+  switch (dtype) {
+    case AVEY_DTYPE_BF16: return launch_bwd_d<__bf16, A>(p, s);
+    case AVEY_DTYPE_F16: return launch_bwd_d<_Float16, A>(p, s);
+    case AVEY_DTYPE_F32: return launch_bwd_d<float, A>(p, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_bwd(const BwdParams& p, int dtype, hipStream_t s) {
-  if (bwd_fast_path(dtype, p.D, p.z)) return launch_bwd16(p, s);
-  switch (dtype) {
-    case AVEY_DTYPE_BF16: return launch_bwd_d<__bf16>(p, s);
-    case AVEY_DTYPE_F16: return launch_bwd_d<_Float16>(p, s);
-    case AVEY_DTYPE_F32: return launch_bwd_d<float>(p, s);
-    default: return hipErrorInvalidValue;
+  switch (bwd_path(dtype, p.D, p.z, p.normalize != 0)) {
+    case BwdPath::Bf16: return launch_bwd16(p, s);
+    case BwdPath::Fp64: return launch_bwd_a<double>(p, dtype, s);
+    default: return launch_bwd_a<float>(p, dtype, s);
   }
 }
 

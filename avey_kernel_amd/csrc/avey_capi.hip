@@ -324,16 +324,16 @@ int64_t avey_bwd_workspace_bytes(const avey_bwd_args* args) {
   BwdParams p;
   const int st = validate_bwd(args, &p);
   if (st != AVEY_OK) return st;
-  return 4 * bwd_workspace_floats(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr,
-                                  bwd_fast_path(args->fwd.dtype, p.D, p.z));
+  return bwd_workspace_bytes(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr,
+                             bwd_path(args->fwd.dtype, p.D, p.z, p.normalize != 0));
 }
 
 int avey_bwd(const avey_bwd_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   BwdParams p;
   const int st = validate_bwd(a, &p);
   if (st != AVEY_OK) return st;
-  const size_t need = 4 * (size_t)bwd_workspace_floats(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr,
-                                                       bwd_fast_path(a->fwd.dtype, p.D, p.z));
+  const size_t need = (size_t)bwd_workspace_bytes(p.B, p.C, p.D, p.dv != nullptr, p.dbias != nullptr,
+                                                  bwd_path(a->fwd.dtype, p.D, p.z, p.normalize != 0));
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255) != 0) return AVEY_ERR_WORKSPACE;
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);

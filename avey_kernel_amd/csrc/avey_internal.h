@@ -45,9 +45,11 @@ struct BwdParams {
 // Largest feature width of the backward kernels (16 accumulator tiles per wave).
 constexpr int64_t kBwdMaxFeatures = 1024;
 
-// bf16 MFMA path of the backward: bf16, D % 8 == 0, 16-byte aligned z_tr.
-bool bwd_fast_path(int dtype, int64_t D, const void* z);
-int64_t bwd_workspace_floats(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, bool fast);
+// Arithmetic of the backward: fp64 for normalised (Avey-B) calls; bf16 MFMA for bf16
+// with D % 8 == 0 and a 16-byte aligned z_tr; fp32 otherwise.
+enum class BwdPath { Fp32, Bf16, Fp64 };
+BwdPath bwd_path(int dtype, int64_t D, const void* z, bool normalize);
+int64_t bwd_workspace_bytes(int64_t B, int64_t C, int64_t D, bool has_v, bool has_bias, BwdPath path);
 hipError_t launch_bwd(const BwdParams& p, int dtype, hipStream_t s);
 
 // Static tile table entry chosen on the host.

@@ -159,12 +159,12 @@ def key_tile_count(query_tile, c, bm, bn, causal, skip=True):
     return -(-c // bn)
 
 
-def row_condition(z_tr, valid=None, *, eps=1e-6, norm_eps=1e-12):
-    """Per-row conditioning of the Avey-B denominator, sum|S_ij| / |sum S_ij + eps|.
+def row_condition(z_tr, valid=None, *, v=None, causal=False, eps=1e-6, norm_eps=1e-12):
+    """Per-row conditioning of the Avey-B denominator, sum_j |P_ij| / |sum_j P_ij + eps|.
 
-    Reports how much a row amplifies rounding (no reference counterpart;
-    derived from ops.py:79-80). S is symmetric, so summing over keys or over
-    queries gives the same values.
+    P is the masked, weighted similarity of ops.py:69-77 (S, times V when given,
+    causal and key masks), summed over keys j. Reports how much a row amplifies
+    rounding (no reference counterpart; derived from ops.py:79-80).
     """
     z = np.array(z_tr, dtype=np.float64, copy=True)
     if valid is not None:
@@ -172,6 +172,10 @@ def row_condition(z_tr, valid=None, *, eps=1e-6, norm_eps=1e-12):
         z = np.where(valid[:, :, None], z, 0.0)
     zn = z / np.maximum(np.sqrt(np.sum(z * z, -1, keepdims=True)), norm_eps)
     s = np.matmul(zn, np.swapaxes(zn, 1, 2))
+    if v is not None:
+        s = s * np.asarray(v, dtype=np.float64)
+    if causal:
+        s = np.tril(s)
     if valid is not None:
         s = np.where(valid[:, None, :], s, 0.0)
     return np.sum(np.abs(s), -1) / np.abs(np.sum(s, -1) + eps)

@@ -7,7 +7,7 @@ Tolerances (compared with the fp64 oracle on identical inputs):
   relative error, which must stay <= 1e-2.
 
 Cases follow the reference's tail shapes and flag combinations
-(tests/test_triton.py:215-249, tests/test_causal_skip.py:80-105): contexts that
+(tests/test_triton.py:126-159, tests/test_causal_skip.py:80-105): contexts that
 cross query / key tile edges, feature widths that cross slice edges, NaN in
 padded rows, every activation; then the five benchmark configurations at full
 size, size-independent properties (bitwise determinism, causal rows blind to

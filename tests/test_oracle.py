@@ -269,17 +269,30 @@ def test_row_condition_closed_forms(z, valid, eps, want):
     np.testing.assert_allclose(orc.row_condition(z, valid, eps=eps)[0], want, rtol=1e-12)
 
 
-def test_row_condition_matches_a_loop_over_keys():
+@pytest.mark.parametrize('use_v,causal', [(False, False), (True, False), (False, True), (True, True)])
+def test_row_condition_matches_a_loop_over_keys(use_v, causal):
     rng = np.random.default_rng(11)
     z = rng.standard_normal((2, 9, 5))
     valid = rng.random((2, 9)) > 0.3
-    got = orc.row_condition(z, valid, eps=0.1)
+    v = rng.uniform(-1, 1, (9, 9)) if use_v else None
+    got = orc.row_condition(z, valid, v=v, causal=causal, eps=0.1)
     for b in range(2):
         for i in range(9):
             zi = z[b, i] if valid[b, i] else np.zeros(5)
-            s = [0.0 if not (valid[b, i] and valid[b, j]) else
-                 float(zi @ z[b, j]) / (np.linalg.norm(zi) * np.linalg.norm(z[b, j])) for j in range(9)]
+            s = [0.0 if not (valid[b, i] and valid[b, j]) or (causal and j > i) else
+                 float(zi @ z[b, j]) / (np.linalg.norm(zi) * np.linalg.norm(z[b, j])) * (v[i, j] if use_v else 1.0)
+                 for j in range(9)]
             assert abs(got[b, i] - sum(map(abs, s)) / abs(sum(s) + 0.1)) < 1e-12 * (1 + got[b, i])
+
+
+def test_row_condition_weights_and_mask_closed_form():
+    # S = [[1, -1], [-1, 1]] with V = [[1, 0.5], [2, 1]]: P = [[1, -0.5], [-2, 1]],
+    # sums 0.5 and -1, so at eps = 0.5 the conditions are 1.5 / 1 and 3 / 0.5;
+    # causal drops P_01, leaving 1 / 1.5 for row 0.
+    z = np.asarray([[[1., 0.], [-2., 0.]]])
+    v = np.asarray([[1., 0.5], [2., 1.]])
+    np.testing.assert_allclose(orc.row_condition(z, v=v, eps=0.5)[0], [1.5, 6.0], rtol=1e-12)
+    np.testing.assert_allclose(orc.row_condition(z, v=v, causal=True, eps=0.5)[0], [2 / 3, 6.0], rtol=1e-12)
 
 
 @pytest.mark.parametrize('causal,normalize,use_v,act', [
