@@ -18,7 +18,8 @@ INCLUDE = os.path.join(REPO_DIR, 'include')
 BUILD_DIR = os.path.join(PKG_DIR, '_build')
 LIB_PATH = os.path.join(PKG_DIR, 'libavey_hip.so')
 SOURCES = ('avey_capi.hip', 'avey_generic.hip', 'avey_fused.hip', 'avey_backward.hip') + tuple(
-    f'avey_fused_bm{bm}_{t}{k}.hip' for k in ('', '_strided') for bm in (64, 32, 16) for t in ('bf16', 'f16'))
+    f'avey_fused_bm{bm}_{t}{k}.hip' for k in ('', '_strided') for bm in (64, 32, 16) for t in ('bf16', 'f16')) + tuple(
+    f'avey_fused_bm16_{t}{k}_eg.hip' for k in ('', '_strided') for t in ('bf16', 'f16'))
 ARCH = 'gfx950'
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32; some of their
@@ -32,8 +33,9 @@ HIP_FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
 # with MFMA results in VGPRs the compiler stops shuttling them through AGPRs
 # (hundreds of v_accvgpr moves per key tile otherwise). The 64-row variants need
 # more than 256 registers and keep the compiler's default split.
-EXTRA_FLAGS = {f'avey_fused_bm{bm}_{t}{k}.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']
-               for bm in (16, 32) for t in ('bf16', 'f16') for k in ('', '_strided')}
+EXTRA_FLAGS = {f'avey_fused_bm{bm}_{t}{k}{e}.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']
+               for bm in (16, 32) for t in ('bf16', 'f16') for k in ('', '_strided') for e in ('', '_eg')
+               if bm == 16 or not e}
 
 
 def hipcc():

@@ -53,6 +53,13 @@ class AveyBwdArgs(ctypes.Structure):
     ]
 
 
+class AveyEnrichedArgs(ctypes.Structure):
+    _fields_ = [
+        ('fwd', AveyFwdArgs), ('x', ctypes.c_void_p), ('w_gate', ctypes.c_void_p), ('b_gate', ctypes.c_void_p),
+        ('model_dim', ctypes.c_int64), ('gate_activation', ctypes.c_int32),
+    ]
+
+
 class AveyFwdPlan(ctypes.Structure):
     _fields_ = [
         ('kernel', ctypes.c_int32), ('block_m', ctypes.c_int32), ('block_n', ctypes.c_int32),
@@ -65,6 +72,7 @@ class AveyFwdPlan(ctypes.Structure):
 EXPORTS = {
     'avey_fwd': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     'avey_fwd_noalloc': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.c_void_p]),
+    'avey_fwd_enriched': (ctypes.c_int, [ctypes.POINTER(AveyEnrichedArgs), ctypes.c_void_p]),
     'avey_fwd_workspace_bytes': (ctypes.c_int64, [ctypes.POINTER(AveyFwdArgs)]),
     'avey_fwd_plan': (ctypes.c_int, [ctypes.POINTER(AveyFwdArgs), ctypes.POINTER(AveyFwdPlan)]),
     'avey_key_tile_count': (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
@@ -76,7 +84,7 @@ EXPORTS = {
     'avey_abi_version': (ctypes.c_int, []),
     'avey_debug_poison_lds': (ctypes.c_int, [ctypes.c_void_p]),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_BYTES = 4 << 20  # AVEY_NOALLOC_SCRATCH_BYTES of include/avey_hip.h
 
 _lib = None
@@ -199,6 +207,55 @@ def launch(z_tr, v, z_tl, bias, valid, out, eps, norm_eps, causal, normalize, ac
     if st > 0:
         raise RuntimeError(f'avey_fwd: HIP error {st}: {status_string(st)}')
     return out
+
+
+def enriched_supported(x, z_tr, w_gate):
+    """True when avey_fwd_enriched covers the call (checked on the host; the library
+    checks again and reports a status otherwise)."""
+    batch, context, features = z_tr.shape
+    d = x.shape[-1]
+    return (z_tr.dtype in (torch.bfloat16, torch.float16) and x.dtype == z_tr.dtype
+            and w_gate.dtype == z_tr.dtype and features % 8 == 0 and features <= 1024
+            and d % 8 == 0 and 8 <= d <= 65536)
+
+
+def launch_enriched(x, w_gate, b_gate, z_tr, v, bias, valid, out, eps, norm_eps, causal, normalize, activation,
+                    gate_activation):
+    """avey_fwd_enriched into ``out`` on the current stream of z_tr's device."""
+    lib = load()
+    valid_u8 = valid.view(torch.uint8) if valid is not None else None
+    fwd = make_args(z_tr, v, None, bias, valid_u8, out, eps, norm_eps, causal, normalize, activation)
+    args = AveyEnrichedArgs(fwd, _ptr(x), _ptr(w_gate), _ptr(b_gate), x.shape[-1],
+                            ACTIVATION_IDS[gate_activation])
+    with torch.cuda.device(z_tr.device):
+        stream = torch.cuda.current_stream(z_tr.device).cuda_stream
+        st = lib.avey_fwd_enriched(ctypes.byref(args), stream)
+    if st < 0:
+        raise ValueError(f'avey_fwd_enriched: {status_string(st)}')
+    if st > 0:
+        raise RuntimeError(f'avey_fwd_enriched: HIP error {st}: {status_string(st)}')
+    return out
+
+
+@torch.library.custom_op('avey_kernels::contextualize_enriched', mutates_args=())
+def contextualize_enriched(x: torch.Tensor, w_gate: torch.Tensor, b_gate: Optional[torch.Tensor],
+                           z_tr: torch.Tensor, v: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+                           valid: Optional[torch.Tensor], eps: float, norm_eps: float, causal: bool,
+                           normalize: bool, activation: str, gate_activation: str) -> torch.Tensor:
+    """contextualize with z_tl = gate_activation(x w_gate^T + b_gate) formed inside the
+    fused kernel (never stored). Forward only; x, w_gate, b_gate are made contiguous."""
+    z_tr = z_tr if readable_in_place(z_tr) else z_tr.contiguous()
+    x, w_gate = x.contiguous(), w_gate.contiguous()
+    b_gate, v, bias, valid = (None if t is None else t.contiguous() for t in (b_gate, v, bias, valid))
+    out = torch.empty_like(z_tr, memory_format=torch.contiguous_format)
+    return launch_enriched(x, w_gate, b_gate, z_tr, v, bias, valid, out, eps, norm_eps, causal, normalize,
+                           activation, gate_activation)
+
+
+@contextualize_enriched.register_fake
+def _contextualize_enriched_fake(x, w_gate, b_gate, z_tr, v, bias, valid, eps, norm_eps, causal, normalize,
+                                 activation, gate_activation):
+    return torch.empty_like(z_tr, memory_format=torch.contiguous_format)
 
 
 @torch.library.custom_op('avey_kernels::contextualize', mutates_args=())

@@ -232,6 +232,9 @@ const char* avey_status_string(int status) {
     case AVEY_ERR_STRIDE: return "z_tr / z_tl row stride below features, or a negative stride";
     case AVEY_ERR_SCRATCH:
       return "the call needs more scratch than avey_fwd_noalloc holds (AVEY_NOALLOC_SCRATCH_BYTES)";
+    case AVEY_ERR_ENRICHED:
+      return "enriched forward: needs z_tl NULL, aligned x / w_gate (/ b_gate), model_dim a multiple of 8 in "
+             "[8, 65536], a known gate activation and a call the fused bf16 / fp16 kernel covers";
     case AVEY_ERR_UNSUPPORTED:
       return "backward needs bf16 / fp16 / fp32, features <= 1024, batch <= 65535 and contiguous operands";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
@@ -347,8 +350,10 @@ int avey_bwd(const avey_bwd_args* a, void* workspace, size_t workspace_bytes, vo
 }  // extern "C"
 
 namespace {
-// Launches the planned kernels of a validated call with `work` as their scratch.
-int run_fwd(const avey_fwd_args* a, const Plan& pl, void* work, hipStream_t s) {
+// Launches the planned kernels of a validated call with `work` as their scratch;
+// with `en`, the 16-row fused kernel that forms the enricher gate.
+int run_fwd(const avey_fwd_args* a, const Plan& pl, void* work, hipStream_t s,
+            const avey_enriched_args* en = nullptr) {
   FwdParams p{};
   p.z = a->z_tr;
   p.v = a->v;
@@ -371,8 +376,45 @@ int run_fwd(const avey_fwd_args* a, const Plan& pl, void* work, hipStream_t s) {
   p.act = a->activation;
   p.eps = a->eps;
   p.norm_eps = a->norm_eps;
+  if (en) {
+    p.xg = en->x;
+    p.wg = en->w_gate;
+    p.bg = en->b_gate;
+    p.dm = en->model_dim;
+    p.gact = en->gate_activation;
+    const hipError_t e = launch_fused_enriched(p, a->dtype, pl, s);
+    return e == hipSuccess ? AVEY_OK : (int)e;
+  }
   const hipError_t e = pl.kernel == 1 ? launch_fused(p, a->dtype, pl, s) : launch_generic(p, a->dtype, pl, s);
   return e == hipSuccess ? AVEY_OK : (int)e;
+}
+
+// Checks of avey_fwd_enriched beyond validate(); fills the 16-row plan.
+int validate_enriched(const avey_enriched_args* en, Plan* pl) {
+  const avey_fwd_args& a = en->fwd;
+  const auto al = [](const void* x, uintptr_t n) { return ((uintptr_t)x & (n - 1)) == 0; };
+  if (a.z_tl || !en->x || !en->w_gate || !al(en->x, 16) || !al(en->w_gate, 16) || !al(en->b_gate, 8))
+    return AVEY_ERR_ENRICHED;
+  if (en->model_dim < 8 || en->model_dim > 65536 || en->model_dim % 8 != 0) return AVEY_ERR_ENRICHED;
+  if (en->gate_activation < AVEY_ACT_IDENTITY || en->gate_activation > AVEY_ACT_GELU) return AVEY_ERR_ENRICHED;
+  *pl = make_plan(a);
+  if (pl->kernel != 1) return AVEY_ERR_ENRICHED;
+  // Every row block of 16: only the 16-row variant forms the gate.
+  pl->bm = 16;
+  pl->threads = fused_threads(16, pl->bd / 32);
+  const int64_t nqt = cdiv(a.context, 16);
+  pl->grid = nqt * a.batch;
+  int64_t steps = 0;
+  for (int64_t qt = 0; qt < nqt; ++qt) steps += key_tiles_for(qt, a.context, 16, 32, a.causal != 0);
+  pl->key_tile_steps = steps * a.batch;
+  const size_t es = elem_size(a.dtype);
+  const size_t nb = (size_t)a.batch * (size_t)a.context * (size_t)a.features * es;
+  const size_t xb = (size_t)a.batch * (size_t)a.context * (size_t)en->model_dim * es;
+  const size_t wb = (size_t)a.features * (size_t)en->model_dim * es;
+  if (overlaps(a.out, nb, en->x, xb) || overlaps(a.out, nb, en->w_gate, wb) ||
+      overlaps(a.out, nb, en->b_gate, (size_t)a.features * es))
+    return AVEY_ERR_ALIAS;
+  return AVEY_OK;
 }
 
 // The current device, checked to be a gfx950 GPU.
@@ -394,6 +436,19 @@ int avey_fwd(const avey_fwd_args* a, void* workspace, size_t workspace_bytes, vo
   const int ds = current_device(&dev);
   if (ds != AVEY_OK) return ds;
   return run_fwd(a, pl, workspace, (hipStream_t)stream);
+}
+
+int avey_fwd_enriched(const avey_enriched_args* en, void* stream) {
+  if (!en) return AVEY_ERR_NULL_POINTER;
+  const int st = validate(&en->fwd);
+  if (st != AVEY_OK) return st;
+  Plan pl;
+  const int se = validate_enriched(en, &pl);
+  if (se != AVEY_OK) return se;
+  int dev = -1;
+  const int ds = current_device(&dev);
+  if (ds != AVEY_OK) return ds;
+  return run_fwd(&en->fwd, pl, nullptr, (hipStream_t)stream, en);
 }
 
 int avey_fwd_noalloc(const avey_fwd_args* a, void* stream) {

@@ -985,6 +985,10 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
 // so the variants compile in parallel.
 template <typename T16, int BM, bool STRIDED>
 hipError_t launch_fused_bm(const FwdParams& p, int nk, int64_t grid, hipStream_t s);
+// The 16-row variants with the enricher gate in the epilogue; defined in
+// avey_fused_bm16_{bf16,f16}[_strided]_eg.hip.
+template <typename T16, bool STRIDED>
+hipError_t launch_fused16_enriched(const FwdParams& p, int nk, int64_t grid, hipStream_t s);
 
 template <typename T16, int BM, int NK, bool STRIDED>
 hipError_t launch_fused_one(const FwdParams& p, int64_t grid, hipStream_t s) {

@@ -14,14 +14,32 @@ static hipError_t launch_fused_t(const FwdParams& p, const Plan& plan, hipStream
   }
 }
 
+static bool strided_operands(const FwdParams& p) {
+  const int64_t row = p.D, item = p.C * p.D;
+  return p.zrs != row || p.zbs != item || (p.gate != nullptr && (p.grs != row || p.gbs != item));
+}
+
 hipError_t launch_fused(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s) {
   // Contiguous operands (the common case) run the instantiations without strides.
-  const int64_t row = p.D, item = p.C * p.D;
-  const bool strided = p.zrs != row || p.zbs != item || (p.gate != nullptr && (p.grs != row || p.gbs != item));
+  const bool strided = strided_operands(p);
   if (dtype == AVEY_DTYPE_BF16)
     return strided ? launch_fused_t<__bf16, true>(p, plan, s) : launch_fused_t<__bf16, false>(p, plan, s);
   if (dtype == AVEY_DTYPE_F16)
     return strided ? launch_fused_t<_Float16, true>(p, plan, s) : launch_fused_t<_Float16, false>(p, plan, s);
+  return hipErrorInvalidValue;
+}
+
+// Only the 16-row variants form the enricher gate (plan.bm is 16 for these calls).
+hipError_t launch_fused_enriched(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s) {
+  if (plan.bm != 16) return hipErrorInvalidConfiguration;
+  const int nk = plan.bd / 32;
+  const bool strided = strided_operands(p);
+  if (dtype == AVEY_DTYPE_BF16)
+    return strided ? launch_fused16_enriched<__bf16, true>(p, nk, plan.grid, s)
+                   : launch_fused16_enriched<__bf16, false>(p, nk, plan.grid, s);
+  if (dtype == AVEY_DTYPE_F16)
+    return strided ? launch_fused16_enriched<_Float16, true>(p, nk, plan.grid, s)
+                   : launch_fused16_enriched<_Float16, false>(p, nk, plan.grid, s);
   return hipErrorInvalidValue;
 }
 

@@ -40,6 +40,15 @@
 // select that zeroes padded rows, one rounding (ops.py:79-91). The gate rows are
 // copied by the S-waves into slot 0 after the last tile, while the M-waves finish
 // the last mixing step.
+//
+// EG (the enricher's gate half fused): there are no gate rows to copy. The M-waves
+// form z_tl = gact(x W_g^T + b_g) for the block's 16 rows: G^T tile t2 = W_g rows
+// (features fw + 16 t2 ..) times the x rows, contracted over the model width on the
+// similarity's MFMA, lands in exactly the lanes and registers of oacc[t2], so the
+// gate never leaves registers. W_g streams through the free key ring after the last
+// key tile: chunk c holds model features 32c .. 32c + 31 of all 128 NK rows (64 bytes
+// a row, at most TILE bytes), copied by the S-waves like a key tile and read by the
+// M-waves after one barrier per chunk. The S-waves also touch the x rows early.
 #pragma once
 
 #include "avey_fused.h"
@@ -154,7 +163,7 @@ struct Small16 {
 
 }  // namespace
 
-template <typename T16, int NK, bool FULL, bool STRIDED, bool HILO>
+template <typename T16, int NK, bool FULL, bool STRIDED, bool HILO, bool EG>
 __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
   typedef G16<NK> Gx;
   constexpr int DS = Gx::DS, NT = Gx::NT, CPR = Gx::CPR, CPRP = Gx::CPRP, G = Gx::G;
@@ -256,6 +265,18 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
       }
     };
 
+    // EG: the block's x rows reach the L2 while the key loop runs (one 4-byte touch per
+    // 128-byte line into the never-read word; rows past 4096 features in part).
+    auto touch_x = [&]() {
+      const uint32_t xrb = (uint32_t)p.dm * 2u, lines = (xrb + 127u) / 128u;
+      const u32x4s r = rows_desc((const char*)p.xg + (int64_t)b * C * xrb, q0, min(C, q0 + 16), xrb, xrb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t line = (uint32_t)(i * 256 + tid);
+        copy4(r, touch_sink, line < 16u * lines ? (line / lines) * xrb + (line % lines) * 128u : kNowhere);
+      }
+    };
+
     // ---- prologue: the 16 query rows into slot R-1 (the two waves of a pair split
     // the P copies of each of their slices, even / odd), key tiles 0 .. R-2 ----------
     {
@@ -270,6 +291,7 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
     // but tile 1's copies is one count.
     copy_tile(0, IC<0>{});
     if (has_gate && touch_t < 1) touch_gate();
+    if constexpr (EG) touch_x();
     if constexpr (R == 3) {
       // Without a tile 1, copies of nothing stand in for it (copy_tile), so that one
       // wait count holds on every path.
@@ -361,6 +383,55 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
         if (t < nkt) interval(t, IC<0>{});
         if (t + 1 < nkt) interval(t + 1, IC<1>{});
       }
+    }
+    if constexpr (EG) {
+      // ---- tail: W_g chunk by chunk through the ring (every slot is free). Chunk c
+      // goes to slot c % R; S-wave wv copies rows 32 NK wv .. + 32 NK - 1 (16 rows per
+      // 1 KB copy: lane l, row l / 4, bytes 16 (l % 4) of the row's 64). A chunk past
+      // the last is copies of nothing, so every step issues the same count.
+      constexpr int CW = 2 * NK, CH = CW <= 8 ? 1 : 2, CP = CW / CH;
+      const uint32_t xrb = (uint32_t)p.dm * 2u;
+      const int ks = (int)((p.dm + 31) / 32);
+      const u32x4s rw = rows_desc((const char*)p.wg, 0, D, xrb, xrb);
+      auto slot_rt = [&](int c) -> char* {
+        const int i = c % R;
+        return i == 0 ? slot0 : (i == 1 ? slot1 : slot2);
+      };
+      auto copy_chunk = [&](int c) {
+        const uint32_t real = c < ks ? 1u : 0u;
+        const uint32_t kb = 64u * (uint32_t)c + 16u * (uint32_t)(lane & 3);
+        char* dst = slot_rt(c) + 1024 * wv * CW;
+#pragma unroll
+        for (int hh = 0; hh < CH; ++hh) {
+          uint32_t o[CP];
+#pragma unroll
+          for (int i = 0; i < CP; ++i) {
+            const uint32_t row = (uint32_t)(16 * (wv * CW + hh * CP + i) + (lane >> 2));
+            o[i] = kb < xrb ? row * xrb + kb : kNowhere;
+          }
+          copies_or_pads<CP>(real, rw, dst + 1024 * CP * hh, touch_sink, o);
+        }
+      };
+      // Chunk c must have landed by barrier c; with three slots chunk c + 1 may still be
+      // in flight there (its slot held chunk c - 2, read before barrier c - 1).
+      auto wait_chunk = [&]() {
+        if constexpr (R == 3)
+          wait_keep(IC<CW>{});
+        else
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+      };
+      copy_chunk(0);
+      if constexpr (R == 3) copy_chunk(1);
+      wait_chunk();
+      lds_barrier();  // chunk 0 (E)
+      for (int c = 1; c < ks; ++c) {
+        copy_chunk(R == 3 ? c + 1 : c);
+        wait_chunk();
+        lds_barrier();  // chunk c
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      lds_barrier();  // the M-waves' reads of the last chunk ended (they reuse slot 0)
+      return;
     }
     // ---- tail: the gate rows of slice 2p + kbs into slot 0 (every slot is free)
     if (has_gate) {
@@ -556,7 +627,7 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
     }
   }
   stage_bc(nkt - 1);
-  lds_barrier();  // E: gate rows copied by the S-waves
+  if constexpr (!EG) lds_barrier();  // E: gate rows copied by the S-waves (EG: the chunk barriers)
   const float dtot = sum_over_groups(den);
   const float rden = p.normalize ? 1.f / (dtot + (float)p.eps) : 1.f;  // signed sum + eps, no clamp
   // ---- epilogue: lane holds query li, features fw + 16 t2 + 4 lg .. +3 --------------
@@ -570,16 +641,60 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
   constexpr int GB = NT <= 12 ? NT : 8;
   // Own loads (bias, validity) retired; the gate rows were waited for by their S-wave.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // EG: G^T = W_g x^T of this wave's slice, chunk by chunk (32 model features) as
+  // the S-waves publish them; the x fragment of the next chunk loads meanwhile. Then
+  // z_tl = gact(G + b_g), in place.
+  f32x4 gacc[EG ? NT : 1];
+  if constexpr (EG) {
+    const uint32_t xrb = (uint32_t)p.dm * 2u;
+    const rsrc_t rx = rows_rsrc((const char*)p.xg + (int64_t)b * C * xrb, q0, C, xrb, xrb);
+    const int ks = (int)((p.dm + 31) / 32);
+    auto xoff = [&](int c) -> uint32_t {
+      const uint32_t kb = 64u * (uint32_t)c + 16u * (uint32_t)lg;
+      return kb < xrb ? (uint32_t)li * xrb + kb : kNowhere;
+    };
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2) gacc[t2] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 xf = ld128(rx, xoff(0));
+    const uint32_t wrow = (uint32_t)(fw + li) * 64u + 16u * (uint32_t)lg;
+    for (int c = 0; c < ks; ++c) {
+      lds_barrier();  // chunk c landed (c = 0: also E)
+      const u32x4 xn = ld128(rx, xoff(c + 1 < ks ? c + 1 : c));
+      const int si = c % R;
+      const char* base = (si == 0 ? slot0 : (si == 1 ? slot1 : slot2)) + wrow;
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2)
+        gacc[t2] = Ops<T16>::mfma32(*reinterpret_cast<const u32x4*>(base + 1024 * t2), xf, gacc[t2]);
+      xf = xn;
+    }
+    // The output staging below writes slot 0 in slices laid out apart from the chunk
+    // rows: every wave's chunk reads end first.
+    lds_barrier();
+    const rsrc_t rbg = make_rsrc(p.bg ? p.bg : p.z, p.bg ? row_bytes : 0u);
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2) {
+      const int f = fw + 16 * t2 + 4 * lg;
+      const u32x2 bgw = ld64(rbg, (FULL || f < D) ? (uint32_t)f * 2u : kNowhere);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t w = bgw[k >> 1];
+        gacc[t2][k] = activate<float>(gacc[t2][k] + ((k & 1) ? Ops<T16>::hi_f(w) : Ops<T16>::to_f(w & 0xffffu)),
+                                      p.gact);
+      }
+    }
+  }
   auto finish = [&](auto act_tag) {
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
     for (int tb = 0; tb < NT; tb += GB) {
       u32x2 gw[GB];
+      if constexpr (!EG) {
 #pragma unroll
-      for (int i = 0; i < GB; ++i) gw[i] = *reinterpret_cast<const u32x2*>(efrag(tb + i));
-      if (!has_gate) {
+        for (int i = 0; i < GB; ++i) gw[i] = *reinterpret_cast<const u32x2*>(efrag(tb + i));
+        if (!has_gate) {
 #pragma unroll
-        for (int i = 0; i < GB; ++i) gw[i] = u32x2{one2, one2};
+          for (int i = 0; i < GB; ++i) gw[i] = u32x2{one2, one2};
+        }
       }
 #pragma unroll
       for (int i = 0; i < GB; ++i) {
@@ -587,11 +702,14 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
         float y[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const uint32_t bword = bw[t2][k >> 1], gword = gw[i][k >> 1];
+          const uint32_t bword = bw[t2][k >> 1], gword = EG ? 0u : gw[i][k >> 1];
           float x = oacc[t2][k] * rden;
           x += (k & 1) ? Ops<T16>::hi_f(bword) : Ops<T16>::to_f(bword & 0xffffu);
           x = activate<float>(x, ACT);
-          x *= (k & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
+          if constexpr (EG)
+            x *= gacc[t2][k];
+          else
+            x *= (k & 1) ? Ops<T16>::hi_f(gword) : Ops<T16>::to_f(gword & 0xffffu);
           y[k] = qok ? x : 0.f;
         }
         *reinterpret_cast<u32x2*>(efrag(t2)) = u32x2{pack2<T16>(y[0], y[1]), pack2<T16>(y[2], y[3])};
@@ -616,33 +734,35 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
   }
 }
 
-template <typename T16, int NK, bool STRIDED>
+template <typename T16, int NK, bool STRIDED, bool EG>
 hipError_t launch_fused16_one(const FwdParams& p, int64_t grid, hipStream_t s) {
   const dim3 g((unsigned)grid), t(512);
   const bool full = p.D == 4 * 32 * NK;
   if (p.normalize != 0) {
     if (full)
-      fused16_kernel<T16, NK, true, STRIDED, true><<<g, t, 0, s>>>(p);
+      fused16_kernel<T16, NK, true, STRIDED, true, EG><<<g, t, 0, s>>>(p);
     else
-      fused16_kernel<T16, NK, false, STRIDED, true><<<g, t, 0, s>>>(p);
+      fused16_kernel<T16, NK, false, STRIDED, true, EG><<<g, t, 0, s>>>(p);
   } else {
     if (full)
-      fused16_kernel<T16, NK, true, STRIDED, false><<<g, t, 0, s>>>(p);
+      fused16_kernel<T16, NK, true, STRIDED, false, EG><<<g, t, 0, s>>>(p);
     else
-      fused16_kernel<T16, NK, false, STRIDED, false><<<g, t, 0, s>>>(p);
+      fused16_kernel<T16, NK, false, STRIDED, false, EG><<<g, t, 0, s>>>(p);
   }
   return hipGetLastError();
 }
 
-template <typename T16, bool STRIDED>
+// EG: the enricher gate formed in the epilogue (avey_fwd_enriched); compiled apart
+// from the plain variants (avey_fused_bm16_*_eg.hip).
+template <typename T16, bool STRIDED, bool EG = false>
 hipError_t launch_fused16(const FwdParams& p, int nk, int64_t grid, hipStream_t s) {
   switch (nk) {
-    case 1: return launch_fused16_one<T16, 1, STRIDED>(p, grid, s);
-    case 2: return launch_fused16_one<T16, 2, STRIDED>(p, grid, s);
-    case 3: return launch_fused16_one<T16, 3, STRIDED>(p, grid, s);
-    case 4: return launch_fused16_one<T16, 4, STRIDED>(p, grid, s);
-    case 6: return launch_fused16_one<T16, 6, STRIDED>(p, grid, s);
-    case 8: return launch_fused16_one<T16, 8, STRIDED>(p, grid, s);
+    case 1: return launch_fused16_one<T16, 1, STRIDED, EG>(p, grid, s);
+    case 2: return launch_fused16_one<T16, 2, STRIDED, EG>(p, grid, s);
+    case 3: return launch_fused16_one<T16, 3, STRIDED, EG>(p, grid, s);
+    case 4: return launch_fused16_one<T16, 4, STRIDED, EG>(p, grid, s);
+    case 6: return launch_fused16_one<T16, 6, STRIDED, EG>(p, grid, s);
+    case 8: return launch_fused16_one<T16, 8, STRIDED, EG>(p, grid, s);
     default: return hipErrorInvalidConfiguration;
   }
 }

@@ -22,6 +22,13 @@ struct FwdParams {
   int64_t grs, gbs;     // z_tl row / batch strides (elements)
   int32_t causal, normalize, act;
   double eps, norm_eps;
+  // Enricher gate (avey_fwd_enriched; gate == nullptr then): z_tl = gact(xg wg^T + bg),
+  // formed per row block inside the 16-row fused kernel and never stored.
+  const void* xg;       // x [B][C][dm], contiguous
+  const void* wg;       // [D][dm]: the enricher weight rows that produce z_tl
+  const void* bg;       // [D] or null
+  int64_t dm;           // model width, a multiple of 8
+  int32_t gact;
 };
 
 // Arguments of the backward kernels. Every [B][C][D] operand is contiguous.
@@ -66,5 +73,7 @@ Plan make_plan(const avey_fwd_args& a);
 
 hipError_t launch_generic(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s);
 hipError_t launch_fused(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s);
+// The 16-row fused kernel with the enricher gate formed in its epilogue (p.wg set).
+hipError_t launch_fused_enriched(const FwdParams& p, int dtype, const Plan& plan, hipStream_t s);
 
 }  // namespace avey

@@ -195,3 +195,57 @@ def avey_b(z_tr: torch.Tensor, *, z_tl=None, bias=None, valid=None, eps=1e-6,
     """
     return _dispatch(z_tr, None, z_tl, bias, valid, eps, norm_eps, False, True, activation,
                      backend, output_tile, autotune)
+
+
+def _enriched(x, w_gate, b_gate, gate_activation, z_tr, v, bias, valid, eps, norm_eps, causal, normalize,
+              activation, backend):
+    if backend not in ('auto', 'hip', 'torch'):
+        raise ValueError("backend must be 'auto', 'hip' or 'torch' for the enriched forward")
+    if gate_activation not in _ACTIVATIONS:
+        raise ValueError(f'unknown gate_activation {gate_activation!r}')
+    if x.dim() != 3 or x.shape[:2] != z_tr.shape[:2] or w_gate.shape != (z_tr.shape[2], x.shape[2]):
+        raise ValueError('x must be [batch, context, d] and w_gate [features, d] for z_tr [batch, context, features]')
+    if b_gate is not None and b_gate.shape != (z_tr.shape[2],):
+        raise ValueError('b_gate must have shape [features]')
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, w_gate, b_gate, z_tr, v, bias))
+    fused_ok = (backend in ('auto', 'hip') and not needs_grad and _fused_device(z_tr)
+                and _hip.enriched_supported(x, z_tr, w_gate))
+    if backend == 'hip' and not fused_ok:
+        raise ValueError('the fused enriched kernel needs bf16 / fp16 ROCm tensors on a gfx950 GPU, '
+                         'features <= 1024 and multiples of 8, and no gradients; use backend="torch"')
+    if not fused_ok:
+        # The composition it replaces: the enricher's gate half, then the op.
+        gate = _activate(F.linear(x.float(), w_gate.float(), None if b_gate is None else b_gate.float()),
+                         gate_activation).to(z_tr.dtype)
+        return _dispatch(z_tr, v, gate, bias, valid, eps, norm_eps, causal, normalize, activation,
+                         'torch' if backend == 'torch' else 'auto', 32, False)
+    _validate(z_tr, v, None, bias, valid, eps, norm_eps, activation, 'auto', 32, False)
+    return torch.ops.avey_kernels.contextualize_enriched(
+        x, w_gate, b_gate, _rows(z_tr), v, bias, valid, float(eps), float(norm_eps), bool(causal),
+        bool(normalize), activation, gate_activation)
+
+
+def avey_enriched(x: torch.Tensor, w_gate: torch.Tensor, z_tr: torch.Tensor, v: torch.Tensor, *, b_gate=None,
+                  gate_activation='relu', bias=None, valid=None, causal=True, norm_eps=1e-12,
+                  activation='identity', backend='auto'):
+    """``avey(z_tr, v, z_tl=gate_activation(x @ w_gate.T + b_gate), ...)`` with the gate
+    formed inside the fused kernel, one [16, features] tile per row block, and never
+    stored. In Avey the enricher's output tail splits into z_tl and z_tr; the static
+    layers around the op (ops.py:4-7 of the reference) stay the caller's, except the
+    gate half of the enricher, which this call takes over from it: the caller passes
+    the enricher's input x and the weight rows (and bias) that produce z_tl.
+    Inference only: with gradients, or where the fused kernel does not apply, it runs
+    the composition (the gate in fp32, rounded to z_tr's type, then ``avey``)."""
+    if v is None:
+        raise ValueError('Avey requires the learned V matrix (v)')
+    return _enriched(x, w_gate, b_gate, gate_activation, z_tr, v, bias, valid, 1e-6, norm_eps, causal, False,
+                     activation, backend)
+
+
+def avey_b_enriched(x: torch.Tensor, w_gate: torch.Tensor, z_tr: torch.Tensor, *, b_gate=None,
+                    gate_activation='relu', bias=None, valid=None, eps=1e-6, norm_eps=1e-12,
+                    activation='identity', backend='auto'):
+    """``avey_b`` with the enricher's gate half fused, as ``avey_enriched``."""
+    return _enriched(x, w_gate, b_gate, gate_activation, z_tr, None, bias, valid, eps, norm_eps, False, True,
+                     activation, backend)

@@ -16,9 +16,11 @@ MI355X ridge (315 flop/B), so its roofline is HBM.
 
 Besides the warm (back-to-back, MALL-resident) figure, every configuration is
 also timed cold: each of ``--cold-calls`` calls follows a 512 MiB write that
-evicts the 256 MB MALL and the L2s. A single call's event span carries launch
-overhead, so the cold kernel time is the warm graph time plus the difference
-between cold and warm single-call spans measured the same way.
+evicts the 256 MB MALL and the L2s. The calls are queued behind a spin kernel,
+so that the GPU never waits for the host inside a span; a single call's event
+span still carries the per-launch overhead the graph hides, so the cold kernel
+time is the warm graph time plus the difference between cold and warm
+single-call spans measured the same way (warm: a 4 KiB write instead).
 
 The CPU baseline times the torch-eager restatement of the reference's path
 (oracle/avey_torch_ref.py, what the reference runs on ROCm, fp32 accumulation,
@@ -61,6 +63,9 @@ def parse_args():
                          'after one plain copy of --copy-mib MiB, whose HBM counters calibrate the '
                          'per-dispatch FETCH_SIZE / WRITE_SIZE readings')
     ap.add_argument('--copy-mib', type=int, default=256)
+    ap.add_argument('--enriched', action='store_true',
+                    help='also time avey_fwd_enriched (the enricher gate formed in the kernel) against '
+                         'the gate GEMM + activation + contextualizer, for C2-C5 behind a d = D/2 enricher')
     ap.add_argument('--backward', action='store_true',
                     help='also time the fused backward (avey_bwd) and forward+backward through autograd '
                          'against autograd over the eager path, for every configuration')
@@ -117,6 +122,10 @@ def measure_single_calls(torch, fn, calls, flush):
     same stream (flush=False: a 4 KiB write, the inputs stay resident)."""
     scratch = torch.empty((512 << 20) if flush else 4096, dtype=torch.uint8, device='cuda')
     evs = []
+    # Every call is enqueued while the GPU spins (about 4 ms at 2.4 GHz), so no span
+    # waits for the host to launch its call, with a small write before it or a large one.
+    torch.cuda.synchronize()
+    torch.cuda._sleep(10_000_000)
     for i in range(calls):
         scratch.fill_(i & 0xFF)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -191,6 +200,53 @@ def measure_config(torch, wl, tag, steps, warmup, cold_calls):
         cold_ms = per_call_ms + max(span_cold - span_warm, 0.0)
         SPANS[tag] = (round(span_cold * 1e3, 3), round(span_warm * 1e3, 3))
     return cfg, inp, flops, nbytes, per_call_ms, wall_ms, eager_ms, cold_ms
+
+
+def measure_enriched(torch, wl, tag, steps, warmup):
+    """avey_fwd_enriched (z_tl formed per row block in the kernel, never stored) against
+    the composition it replaces: the enricher's gate GEMM (hipBLASLt, bf16 out), its
+    ReLU, then the contextualizer reading z_tl. Model width d = D / 2; both in one HIP
+    graph of back-to-back calls. Also the contextualizer alone with a stored z_tl."""
+    import torch.nn.functional as F
+    from avey_kernel_amd import avey_b_enriched, avey_enriched
+    cfg = wl.CONFIGS[tag]
+    inp = wl.make_inputs(cfg, device='cuda')
+    d = cfg.features // 2
+    g = torch.Generator().manual_seed(200 + cfg.seed)
+    x = torch.randn(cfg.batch, cfg.context, d, generator=g).to(cfg.dtype).to('cuda')
+    w = (torch.randn(cfg.features, d, generator=g) / d ** 0.5).to(cfg.dtype).to('cuda')
+    bg = (torch.randn(cfg.features, generator=g) * 0.1).to(cfg.dtype).to('cuda')
+    normalize = cfg.op == 'avey_b'
+    v = inp['v'] if not normalize else None
+    kw = dict(bias=inp['bias'], valid=inp['valid'])
+
+    def fused():
+        if normalize:
+            return avey_b_enriched(x, w, inp['z_tr'], b_gate=bg, gate_activation='relu', backend='hip', **kw)
+        return avey_enriched(x, w, inp['z_tr'], v, b_gate=bg, gate_activation='relu', causal=cfg.causal,
+                             backend='hip', **kw)
+
+    def unfused():
+        gate = F.relu(F.linear(x, w, bg))
+        return wl.call(cfg, dict(inp, z_tl=gate), backend='hip')
+
+    def op_only():
+        return wl.call(cfg, inp, backend='hip')
+
+    with torch.inference_mode():
+        fused_ms, _ = measure_graph(torch, fused, steps, warmup)
+        unfused_ms, _ = measure_graph(torch, unfused, steps, warmup)
+        op_ms, _ = measure_graph(torch, op_only, steps, warmup)
+    es = 2
+    n = cfg.batch * cfg.context
+    row = {'config': cfg.name, 'model_dim': d, 'fused_us': round(fused_ms * 1e3, 2),
+           'gemm_act_op_us': round(unfused_ms * 1e3, 2), 'op_alone_us': round(op_ms * 1e3, 2),
+           'speedup': round(unfused_ms / fused_ms, 3),
+           'hbm_bytes_removed': 2 * n * cfg.features * es,  # z_tl written by the GEMM, read by the op
+           'hbm_bytes_added': n * d * es}                   # x read by the op
+    del inp, x, w
+    torch.cuda.empty_cache()
+    return row
 
 
 def measure_backward(torch, wl, tag, steps, warmup):
@@ -362,7 +418,8 @@ def main():
         'us_per_call_cold_mall_flushed': None if cold_ms is None else round(cold_ms * 1e3, 3),
         'tflops_cold': None if cold_ms is None else round(flops / (cold_ms * 1e-3) / 1e12, 2),
         'cold_method': f'median of {args.cold_calls} single calls after a 512 MiB write, minus the median of '
-                       f'{args.cold_calls} single calls after a 4 KiB write, added to the warm graph time',
+                       f'{args.cold_calls} single calls after a 4 KiB write, added to the warm graph time; '
+                       f'both sets queued behind a spin kernel so that no span includes host launch time',
         'single_call_spans_us_cold_warm': SPANS.get(cfg.tag),
         'wall_ms_per_step': round(wall_ms, 5),
         'useful_flops': flops,
@@ -399,6 +456,14 @@ def main():
             rows.append(row)
             log(f'[bench] {json.dumps(row)}')
     extra['configs'] = rows
+
+    if args.enriched:
+        enr_rows = []
+        for tag in ('C2', 'C3', 'C4', 'C5'):
+            row = measure_enriched(torch, wl, tag, max(args.steps // 2, 20), min(args.warmup, 5))
+            enr_rows.append(row)
+            log(f'[bench] enriched {json.dumps(row)}')
+        extra['enriched'] = enr_rows
 
     bwd_rows = []
     if args.backward:

@@ -16,6 +16,10 @@
  *                         the causal tile-skip rule; host-only.
  *   - avey_fwd_noalloc    avey_fwd without allocation; no reference counterpart
  *                         (for callers that cannot allocate device memory).
+ *   - avey_fwd_enriched   avey_fwd with the enricher's gate half fused: replaces the
+ *                         caller's enricher GEMM for z_tl and the z_tl tensor the op
+ *                         receives (the static layers around the op, ops.py:4-7;
+ *                         the reference takes z_tl as stored, ops.py:109-113).
  *   - avey_bwd            replaces autograd over the eager path for the
  *                         gradients (avey_kernels/ops.py:96-106 and :61-91).
  *   - avey_fwd_workspace_bytes, avey_bwd_workspace_bytes, avey_status_string, avey_abi_version,
@@ -47,7 +51,7 @@
 extern "C" {
 #endif
 
-#define AVEY_ABI_VERSION 4
+#define AVEY_ABI_VERSION 5
 
 /* Element type of z_tr / z_tl / v / bias / out. */
 enum avey_dtype {
@@ -80,6 +84,7 @@ enum avey_status {
   AVEY_ERR_STRIDE = -10,          /* a row stride below features, or a negative stride */
   AVEY_ERR_UNSUPPORTED = -11,     /* backward: fp64, features > 1024, batch > 65535 or strided operands */
   AVEY_ERR_SCRATCH = -12,         /* avey_fwd_noalloc: the call needs more than AVEY_NOALLOC_SCRATCH_BYTES */
+  AVEY_ERR_ENRICHED = -13,        /* avey_fwd_enriched: see avey_enriched_args */
 };
 
 typedef struct avey_fwd_args {
@@ -150,6 +155,27 @@ int avey_fwd(const avey_fwd_args* args, void* workspace, size_t workspace_bytes,
  * host threads) race and must be serialised by the caller. */
 #define AVEY_NOALLOC_SCRATCH_BYTES (4u << 20)
 int avey_fwd_noalloc(const avey_fwd_args* args, void* stream);
+/* The forward with the enricher's gate half fused (ABI 5). In Avey the enricher
+ * z = act_e(x W_e^T + b_e) produces the op's two inputs as halves of its tail,
+ * z_tl and z_tr. Here the caller still computes z_tr (every row block reads all of
+ * it as keys); z_tl = gate_activation(x w_gate^T + b_gate) is formed for each block of
+ * 16 query rows inside the fused kernel and never stored, which saves the enricher
+ * writing it and the op reading it (2 * batch * context * features elements).
+ * Requirements (else AVEY_ERR_ENRICHED): fwd.z_tl NULL; x and w_gate non-NULL and
+ * 16-byte aligned, b_gate NULL or 8-byte aligned, all of fwd.dtype; model_dim a
+ * multiple of 8 in [8, 65536]; gate_activation an avey_activation id; and a call the
+ * fused kernel covers (bf16 / fp16, features <= 1024 and a multiple of 8, the
+ * layout rules of avey_fwd_plan). Needs no workspace. */
+typedef struct avey_enriched_args {
+  avey_fwd_args fwd;       /* as for avey_fwd, with z_tl NULL */
+  const void* x;           /* [batch][context][model_dim], contiguous: the enricher's input */
+  const void* w_gate;      /* [features][model_dim]: the enricher weight rows of z_tl */
+  const void* b_gate;      /* [features] or NULL: their bias */
+  int64_t model_dim;
+  int32_t gate_activation; /* enum avey_activation, the enricher's activation */
+} avey_enriched_args;
+int avey_fwd_enriched(const avey_enriched_args* args, void* stream);
+
 /* Device scratch bytes avey_fwd needs for these arguments (0 when none). Host-only. */
 int64_t avey_fwd_workspace_bytes(const avey_fwd_args* args);
 

@@ -35,6 +35,8 @@ Pinning (each check lives in ``tests/test_oracle.py``):
 * ``key_tile_count``: the reference's closed-form table
   (``tests/test_causal_skip.py:52-60``) and a brute-force count of tiles
   holding at least one allowed (query, key) pair.
+* ``enricher_gate``: ``torch.nn.functional.linear`` in fp64 followed by the
+  activations above, and a hand-computed 2 x 2 case.
 * ``row_condition`` (a diagnostic printed next to Avey-B results; no test
   bound depends on it except the fp32 subset of rows held to 1e-5): closed
   forms on rows with similarities +-1 / 0 (cancelling sums, eps inside the
@@ -76,6 +78,20 @@ def activate(x, activation):
         inner = _GELU_K * (x + 0.044715 * x * x * x)
         return 0.5 * x * (1.0 + np.tanh(inner))
     raise ValueError(f'unknown activation {activation!r}')
+
+
+def enricher_gate(x, w_gate, b_gate=None, activation='relu'):
+    """z_tl as the enricher produces it: activation(x @ w_gate^T + b_gate).
+
+    The static layer just before the op (the reference leaves it to the caller,
+    ``avey_kernels/ops.py:4-7``): in Avey the enricher's output tail splits into
+    z_tl and z_tr, so z_tl is the product of x with the enricher weight rows of
+    that half. ``x``: [..., d]; ``w_gate``: [features, d] (nn.Linear layout).
+    """
+    y = np.matmul(x, np.swapaxes(w_gate, -1, -2))
+    if b_gate is not None:
+        y = y + b_gate
+    return activate(y, activation)
 
 
 def normalize_rows(z, norm_eps):

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
     assert declared == set(_hip.EXPORTS), declared ^ set(_hip.EXPORTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.avey_abi_version() == _hip.ABI_VERSION == 4
+    assert lib.avey_abi_version() == _hip.ABI_VERSION == 5
 
 
 def _args(**over):
@@ -110,6 +110,10 @@ def test_backward_workspace_layout():
     assert fast == 4 * (2 * up(b * c) + up(b * c * d8) + 2 * up(b * d8 * cp // 2) + up(b * c * d8 // 2))
     assert lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args(features=d8, dtype=1))) == \
         4 * (2 * up(b * c) + 2 * up(b * c * d8))
+    # Avey-B (normalize) computes in fp64 whatever the type: 8-byte parts, no bf16 copies.
+    for dt, dd in ((2, d8), (0, d)):
+        assert lib.avey_bwd_workspace_bytes(ctypes.byref(_bwd_args(features=dd, dtype=dt, normalize=1))) == \
+            8 * (2 * up(b * c) + 2 * up(b * c * dd))
     # The launch refuses a short or misaligned workspace before touching a device.
     assert lib.avey_bwd(ctypes.byref(full), None, 0, None) == -6
     assert lib.avey_bwd(ctypes.byref(full), (1 << 46) + 4, 1 << 30, None) == -6
@@ -118,6 +122,31 @@ def test_backward_workspace_layout():
 def test_null_args_pointer():
     lib = _lib()
     assert lib.avey_fwd(None, None, 0, None) == -1
+    assert lib.avey_fwd_enriched(None, None) == -1
+
+
+def _enriched_args(x=1 << 44, w_gate=1 << 45, b_gate=None, model_dim=384, gate_activation=1, **over):
+    base = dict(features=768, context=256, batch=4)
+    base.update(over)
+    return _hip.AveyEnrichedArgs(_args(**base), x, w_gate, b_gate, model_dim, gate_activation)
+
+
+@pytest.mark.parametrize('over,code', [
+    (dict(batch=0), -2), (dict(activation=6), -4),            # checks of the op itself come first
+    (dict(z_tl=1 << 41), -13),                                 # the gate is formed, not passed
+    (dict(x=None), -13), (dict(w_gate=None), -13),
+    (dict(x=(1 << 44) + 8), -13), (dict(b_gate=(1 << 46) + 2), -13),   # alignment
+    (dict(model_dim=0), -13), (dict(model_dim=388), -13), (dict(model_dim=65544), -13),
+    (dict(gate_activation=5), -13),
+    (dict(dtype=0), -13), (dict(features=1032), -13),          # fp32, wider than the fused kernel
+    (dict(features=770), -13),                                 # rows of a multiple of 8 only
+    (dict(x=(1 << 40) + (1 << 36) + 64), -9),                  # out inside x
+])
+def test_enriched_argument_errors(over, code):
+    lib = _lib()
+    args = _enriched_args(**over)
+    assert lib.avey_fwd_enriched(ctypes.byref(args), None) == code
+    assert lib.avey_status_string(code).decode() not in ('', 'unknown status')
 
 
 def test_key_tile_count_follows_reference_table():

@@ -323,3 +323,25 @@ def test_torch_restatement_matches_numpy_oracle(causal, normalize, use_v, act):
                                  gg.double().numpy(), bb.double().numpy(), valid.numpy(), acc=np.float32, **kw)
         tol = 1e-5 if dt == torch.float32 else 1e-2
         np.testing.assert_allclose(got.double().numpy(), want, rtol=tol, atol=tol)
+
+
+def test_enricher_gate_hand_case_and_torch_linear():
+    # x = [1, 2], W = [[1, -1], [0.5, 0.25]], b = [0.5, -1]: x W^T + b = [-0.5, 0], relu -> [0, 0],
+    # identity -> [-0.5, 0], relu2 of [-0.5, 3] (b = [0.5, 2]) -> [0, 9].
+    x = np.array([[1.0, 2.0]])
+    w = np.array([[1.0, -1.0], [0.5, 0.25]])
+    np.testing.assert_array_equal(orc.enricher_gate(x, w, np.array([0.5, -1.0]), 'identity'), [[-0.5, 0.0]])
+    np.testing.assert_array_equal(orc.enricher_gate(x, w, np.array([0.5, -1.0]), 'relu'), [[0.0, 0.0]])
+    np.testing.assert_array_equal(orc.enricher_gate(x, w, np.array([0.5, 2.0]), 'relu2'), [[0.0, 9.0]])
+    g = torch.Generator().manual_seed(5)
+    xt = torch.randn(2, 7, 24, generator=g, dtype=torch.float64)
+    wt = torch.randn(40, 24, generator=g, dtype=torch.float64)
+    bt = torch.randn(40, generator=g, dtype=torch.float64)
+    for act, fn in (('relu', torch.relu), ('silu', torch.nn.functional.silu),
+                    ('gelu', lambda t: torch.nn.functional.gelu(t, approximate='tanh'))):
+        want = fn(torch.nn.functional.linear(xt, wt, bt)).numpy()
+        np.testing.assert_allclose(orc.enricher_gate(xt.numpy(), wt.numpy(), bt.numpy(), act), want,
+                                   rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(orc.enricher_gate(xt.numpy(), wt.numpy(), None, 'identity'),
+                               torch.nn.functional.linear(xt, wt).numpy(), rtol=1e-12, atol=1e-12)
+
