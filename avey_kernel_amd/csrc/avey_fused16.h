@@ -249,11 +249,16 @@ __global__ __launch_bounds__(512, 1) void fused16_kernel(FwdParams p) {
       __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
     };
     // The gate rows reach the L2 ahead of the epilogue's copy (one 4-byte touch per
-    // 128-byte line into a never-read word): at the start when the whole grid's gate
-    // fits the L2s with room to spare, else three key tiles before the tail.
+    // 128-byte line into a never-read word). When the whole grid's gate fits the L2s
+    // with room to spare, the touches wait until a few tiles of the loop have been
+    // issued, so that they do not compete with the prologue's loads, which every
+    // workgroup issues at once (C2: touching in the prologue 13.29 us per call,
+    // interval 1 13.28, interval 3 for workgroups of more than 4 key tiles and 1 for 3-4
+    // tiles 12.53, on one box); light workgroups still touch at the start. Larger grids
+    // touch three key tiles before the tail.
     constexpr int kTouchLead = 3;
     const bool gate_fits = (uint64_t)B * (uint64_t)C * row_bytes <= (8ull << 20);
-    const int touch_t = gate_fits ? 0 : nkt - kTouchLead;
+    const int touch_t = gate_fits ? (nkt > 4 ? 3 : (nkt > 2 ? 1 : 0)) : nkt - kTouchLead;
     auto touch_gate = [&]() {
       const u32x4s r = rows_desc(gb, q0, min(C, q0 + 16), gstride, row_bytes);
       constexpr int kLines = 4 * 32 * NK * 2 / 128;
