@@ -84,7 +84,7 @@ __device__ __forceinline__ float activate<float>(float x, int act) {
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Waves of the fused kernel's (BM query rows, NK 32-feature steps per slice)
-// variants. The 16-row ones split roles over 8 waves (4 product waves, 4 helpers);
+// variants. The 16-row ones split roles over 8 waves (4 similarity waves, 4 mixing);
 // 32- and 64-row ones split their query blocks over 8 waves where a wave's half of
 // the state fits 256 registers (up to 192 features per slice with 32 rows, 128
 // with 64), and otherwise run 4 waves of 512 registers.

@@ -733,23 +733,19 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     }
   };
 
-  // ---- interval-2 publication: A(t)'s partial S^T (product waves) and the tile's key
-  // reciprocals (reduction waves: every one computes the same values, lanes 32..63
-  // repeating 0..31, so no wave waits on a branch here) ---------------------------------
-  auto publish = [&](auto mma, auto red) {
-    if constexpr (decltype(mma)::value) {
+  // ---- interval-2 publication: A(t)'s partial S^T and the tile's key reciprocals
+  // (every wave computes the same reciprocals, lanes 32..63 repeating 0..31, so no
+  // wave waits on a branch here) ---------------------------------------------------
+  auto publish = [&]() {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < QBW; ++qb) sx[w][kb][qb0 + qb][lane] = sacc[kb][qb];
-    }
-    if constexpr (decltype(red)::value) {
-      const int k = lane & (kBN - 1);
-      const float n = (sm.nxp[0][k] + sm.nxp[1][k]) + (sm.nxp[2][k] + sm.nxp[3][k]);
-      // A float store: an element assignment to the vector would be a read-modify-
-      // write of all 16 bytes, racing with the lanes that own the other three keys.
-      reinterpret_cast<float*>(sm.rk)[k] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
-    }
+      for (int qb = 0; qb < QBW; ++qb) sx[w][kb][qb0 + qb][lane] = sacc[kb][qb];
+    const int k = lane & (kBN - 1);
+    const float n = (sm.nxp[0][k] + sm.nxp[1][k]) + (sm.nxp[2][k] + sm.nxp[3][k]);
+    // A float store: an element assignment to the vector would be a read-modify-
+    // write of all 16 bytes, racing with the lanes that own the other three keys.
+    reinterpret_cast<float*>(sm.rk)[k] = n < 0.f ? 0.f : (n > eps2 ? __builtin_amdgcn_rsqf(n) : inv_eps);
   };
 
   // s_waitcnt encodings (gfx9: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at
@@ -827,7 +823,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     // F.normalize divides by max(||q||, norm_eps); 0 marks padded / out-of-range rows.
     sm.rq[tid] = ss < 0.f ? 0.f : (ss > eps2 ? __builtin_amdgcn_rsqf(ss) : inv_eps);
   }
-  publish(TT{}, TT{});
+  publish();
   if constexpr (SPLIT) stage_t(IC<0>{});
   if constexpr (QS) wait_next_tile(nkt == 1);
   lds_barrier();
@@ -848,7 +844,7 @@ __global__ __launch_bounds__((Geo<BM, NK>::THREADS), 1) void fused_fwd_kernel(Fw
     stage_a(t, cur, t + R - 1, IC<PREV>{}, refill, IC<KA>{});
     lds_barrier();
     stage_c(t + R - 1, IC<PREV>{}, refill, TT{});
-    publish(TT{}, TT{});
+    publish();
     if constexpr (SPLIT) {
       // T(t) overwrites the operands C just used: keep the scheduler from hoisting
       // its reads above C's MFMAs (two live copies would not fit the registers).
