@@ -164,6 +164,48 @@ def test_make_fx_records_exactly_one_fused_call():
     assert len(calls) == 1
 
 
+def test_enriched_op_traces_as_one_opaque_call():
+    # avey_kernels::contextualize_enriched (the enricher gate fused) has a fake too.
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    def fn(x, w, z):
+        return torch.ops.avey_kernels.contextualize_enriched(x, w, None, z, None, None, None, 1e-6, 1e-12, True,
+                                                             False, 'identity', 'relu')
+
+    args = (torch.empty(2, 35, 24, dtype=torch.bfloat16), torch.empty(40, 24, dtype=torch.bfloat16),
+            torch.empty(2, 35, 40, dtype=torch.bfloat16))
+    graph = make_fx(fn, tracing_mode='fake')(*args)
+    calls = [n for n in graph.graph.nodes if 'contextualize_enriched' in str(n.target)]
+    assert len(calls) == 1
+    out = [n for n in graph.graph.nodes if n.op == 'output'][0].args[0]
+    assert tuple(out.meta['val'].shape) == (2, 35, 40)
+
+
+def test_enriched_on_the_cpu_runs_the_composition():
+    # Off the GPU (and with gradients) avey_enriched is the enricher's gate half
+    # followed by the op, which the oracle restates in fp64.
+    import numpy as np
+    from avey_kernel_amd import avey_b_enriched, avey_enriched
+    from oracle import avey_oracle as orc
+    g = torch.Generator().manual_seed(3)
+    x, w, bg = torch.randn(2, 9, 16, generator=g), torch.randn(12, 16, generator=g), torch.randn(12, generator=g)
+    z, v = torch.randn(2, 9, 12, generator=g), torch.randn(9, 9, generator=g)
+    for normalize in (False, True):
+        gate = orc.enricher_gate(x.double().numpy(), w.double().numpy(), bg.double().numpy(), 'silu')
+        want = orc.contextualize(z.double().numpy(), None if normalize else v.double().numpy(), gate,
+                                 eps=1e-6, norm_eps=1e-12, causal=not normalize, normalize=normalize,
+                                 activation='identity')
+        got = (avey_b_enriched(x, w, z, b_gate=bg, gate_activation='silu') if normalize
+               else avey_enriched(x, w, z, v, b_gate=bg, gate_activation='silu'))
+        np.testing.assert_allclose(got.double().numpy(), want, rtol=1e-4, atol=1e-4)
+    with pytest.raises(ValueError):
+        avey_enriched(x, w, z, v, gate_activation='tanh')
+    with pytest.raises(ValueError):
+        avey_enriched(x, w[:, :8], z, v)
+    with pytest.raises(ValueError):
+        avey_enriched(x, w, z, v, backend='triton')
+
+
 # The drop-in package: a reference caller's imports (`from avey_kernels import avey,
 # avey_b`, avey_kernels/__init__.py:3-5; `avey_kernels.ops.avey`, ops.py:117-147)
 # resolve to this build and give the reference's known answers.

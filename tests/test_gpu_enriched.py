@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from avey_kernel_amd import avey, avey_b, avey_b_enriched, avey_enriched
+from avey_kernel_amd import avey, avey_b_enriched, avey_enriched
 from conftest import gpu_available
 from oracle import avey_oracle as orc
 
@@ -154,3 +154,26 @@ def test_enriched_without_the_fused_kernel_runs_the_composition():
     out = avey_enriched(c['x'], c['w'], zg, c['v'], **kw)
     out.float().sum().backward()
     assert zg.grad is not None and torch.isfinite(zg.grad).all()
+
+
+def test_enriched_hip_graph_replays_match_eager():
+    # avey_fwd_enriched allocates nothing and issues no memset, so it can be captured;
+    # every replay, with eager work between them, gives the eager call's bits.
+    c = _case(2, 96, 384, 128, torch.bfloat16, seed=19, valid=True)
+    run = lambda: _run(c, causal=True, normalize=False, act='gelu', gate_act='relu')  # noqa: E731
+    eager = run().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()  # warm-up on the capture stream (allocator pools)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = run()
+    for rep in range(3):
+        junk = torch.randn(1 << 20, device=DEV) * rep  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        del junk
+        assert torch.equal(static, eager), f'replay {rep}'
