@@ -177,3 +177,17 @@ def test_enriched_hip_graph_replays_match_eager():
         torch.cuda.synchronize()
         del junk
         assert torch.equal(static, eager), f'replay {rep}'
+
+
+def test_enriched_auto_takes_the_composition_where_the_plan_uses_taller_blocks():
+    # B 64, C 256, D 512 Avey-B: the plan runs 64-row workgroups there (256 of them), so
+    # backend='auto' composes (gate GEMM, then the op); the result meets the same bound
+    # either way.
+    from avey_kernel_amd import _hip
+    c = _case(64, 256, 512, 128, torch.bfloat16, seed=23, use_v=False)
+    assert _hip.plan((64, 256, 512), torch.bfloat16, causal=False, normalize=True, has_bias=True)['block_m'] == 64
+    kw = dict(causal=False, normalize=True, act='identity', gate_act='relu')
+    want = _oracle(c, **kw)
+    auto = avey_b_enriched(c['x'], c['w'], c['z'], b_gate=c['bg'], bias=c['bias'], gate_activation='relu')
+    _check(auto, want, torch.bfloat16, 'auto (composition)')
+    _check(_run(c, **kw), want, torch.bfloat16, 'hip (enriched kernel)')
