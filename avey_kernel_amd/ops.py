@@ -212,12 +212,14 @@ def _enriched(x, w_gate, b_gate, gate_activation, z_tr, v, bias, valid, eps, nor
     fused_ok = (backend in ('auto', 'hip') and not needs_grad and _fused_device(z_tr)
                 and _hip.enriched_supported(x, z_tr, w_gate))
     if backend == 'auto' and fused_ok:
-        # The enriched kernel is the 16-row one; where the plan would run 64- or 32-row
-        # workgroups (they read the gate weights a quarter / half as often), the
-        # composition is faster, so 'auto' takes it there.
+        # The enriched kernel is the 16-row one, and each of its workgroups streams all
+        # of the gate weights. It pays where the plan runs 16-row workgroups in one
+        # round over the 256 CUs (C2: 26.1 against 31.8 us); with 32- or 64-row
+        # workgroups (which read the weights a half / quarter as often) or a second
+        # round (C4) the composition is faster, so 'auto' takes it there.
         pl = _hip.plan(tuple(z_tr.shape), z_tr.dtype, causal=causal, normalize=normalize, activation=activation,
                        has_v=v is not None, has_bias=bias is not None, has_valid=valid is not None)
-        fused_ok = pl['kernel'] == 'fused_mfma' and pl['block_m'] == 16
+        fused_ok = pl['kernel'] == 'fused_mfma' and pl['block_m'] == 16 and pl['grid'] <= 256
     if backend == 'hip' and not fused_ok:
         raise ValueError('the fused enriched kernel needs bf16 / fp16 ROCm tensors on a gfx950 GPU, '
                          'features <= 1024 and multiples of 8, and no gradients; use backend="torch"')
@@ -243,8 +245,8 @@ def avey_enriched(x: torch.Tensor, w_gate: torch.Tensor, z_tr: torch.Tensor, v: 
     gate half of the enricher, which this call takes over from it: the caller passes
     the enricher's input x and the weight rows (and bias) that produce z_tl.
     Inference only: with gradients, where the fused kernel does not apply, or (with
-    ``backend='auto'``) where the plan runs 32- or 64-row workgroups, it runs the
-    composition (the gate in fp32, rounded to z_tr's type, then ``avey``);
+    ``backend='auto'``) where the plan runs 32- or 64-row workgroups or more than one
+    round of them, it runs the composition (the gate in fp32, rounded to z_tr's type, then ``avey``);
     ``backend='hip'`` always runs the enriched kernel."""
     if v is None:
         raise ValueError('Avey requires the learned V matrix (v)')
