@@ -96,6 +96,36 @@ template <> struct Io<double> {
   __device__ static f64x4 four(const double* p) { return *(const f64x4*)p; }
 };
 
+// Guarded loads without a branch. Written as `ok ? p[i] : other`, a load the compiler
+// cannot prove in bounds goes into a branch that waits for it before the branches
+// join: one memory round trip per element. Here the load always goes out (to element
+// 0 when !ok, which every caller's array holds) and the result is selected, so a
+// group of loads shares one wait.
+template <typename T>
+__device__ __forceinline__ T ld_sel(const T* p, int64_t i, bool ok, T other) {
+  const T v = p[ok ? i : 0];
+  return ok ? v : other;
+}
+
+__device__ __forceinline__ bool row_valid(const uint8_t* valid, int64_t b, int64_t C, int64_t row) {
+  const bool in = row < C;
+  if (!valid) return in;
+  return in & (valid[in ? b * C + row : 0] != 0);
+}
+
+__device__ __forceinline__ float inv_norm(const float* nrm, int64_t idx, float norm_eps) {
+  return 1.f / fmaxf(nrm[idx], norm_eps);
+}
+__device__ __forceinline__ double inv_norm(const double* nrm, int64_t idx, double norm_eps) {
+  return 1.0 / fmax(nrm[idx], norm_eps);
+}
+// 1 / max(||row||, norm_eps) when ok, else 0 (branch-free, as ld_sel).
+template <typename A>
+__device__ __forceinline__ A inv_norm_sel(const A* nrm, int64_t idx, bool ok, A norm_eps) {
+  const A x = inv_norm(nrm, ok ? idx : 0, norm_eps);
+  return ok ? x : A(0);
+}
+
 // Four consecutive features d..d+3 of one row (zero past D), converted to A. `vec`:
 // rows are 4-element aligned (D % 4 == 0), so a vector load is in bounds when d + 4 <= D.
 template <typename A, typename T>
@@ -110,19 +140,46 @@ __device__ __forceinline__ v4<A> row4(const T* row, int d, int D, bool vec) {
 }
 
 // 16 x 16 block of A B^T contracted over D features. A row lr of the block is
-// `a` (scaled by sa), B row lr is `b` (scaled by sb); a null row contributes
-// zeros and is not read. Lane (lg, lr) feeds features 16s + 4lg + t at sub-step
-// t of step s to both operands (any bijection of the contracted index gives the
-// same sum), so every load is four consecutive features. Result: lane holds
-// C[acc_row<A>(lg, i)][lr], i = 0..3.
+// `a` (scaled by sa), B row lr is `b` (scaled by sb); both are always readable rows,
+// taken as zeros where !aok / !bok. Lane (lg, lr) feeds features 16s + 4lg + t at
+// sub-step t of step s to both operands (any bijection of the contracted index gives
+// the same sum), so every load is four consecutive features. With 4-element aligned
+// rows, the loads of U steps go out before their MFMAs and no load sits in a branch
+// (see ld_sel). Result: lane holds C[acc_row<A>(lg, i)][lr], i = 0..3.
 template <typename A, typename TA, typename TB>
-__device__ __forceinline__ v4<A> row_dot(const TA* a, A sa, const TB* b, A sb, int D, bool vec, int lg) {
+__device__ __forceinline__ v4<A> row_dot(const TA* a, bool aok, A sa, const TB* b, bool bok, A sb, int D, bool vec,
+                                         int lg) {
   v4<A> c = {A(0), A(0), A(0), A(0)};
   const int steps = (D + 15) >> 4;
+  if (vec) {
+    constexpr int U = sizeof(A) == 8 ? 2 : 4;
+    for (int s0 = 0; s0 < steps; s0 += U) {
+      decltype(Io<TA>::four(a)) x[U];
+      decltype(Io<TB>::four(b)) y[U];
+      bool xo[U], yo[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int d = 16 * (s0 + u) + 4 * lg;
+        const bool in = s0 + u < steps && d < D;  // D % 4 == 0: then d + 4 <= D
+        x[u] = Io<TA>::four(a + (in ? d : 0));
+        y[u] = Io<TB>::four(b + (in ? d : 0));
+        xo[u] = in && aok;
+        yo[u] = in && bok;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (s0 + u >= steps) break;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          c = mfma4((xo[u] ? (A)x[u][t] : A(0)) * sa, (yo[u] ? (A)y[u][t] : A(0)) * sb, c);
+      }
+    }
+    return c;
+  }
   for (int s = 0; s < steps; ++s) {
     const int d = 16 * s + 4 * lg;
-    v4<A> x = a ? row4<A, TA>(a, d, D, vec) : v4<A>{A(0), A(0), A(0), A(0)};
-    v4<A> y = b ? row4<A, TB>(b, d, D, vec) : v4<A>{A(0), A(0), A(0), A(0)};
+    v4<A> x = aok ? row4<A, TA>(a, d, D, false) : v4<A>{A(0), A(0), A(0), A(0)};
+    v4<A> y = bok ? row4<A, TB>(b, d, D, false) : v4<A>{A(0), A(0), A(0), A(0)};
 #pragma unroll
     for (int t = 0; t < 4; ++t) c = mfma4(x[t] * sa, y[t] * sb, c);
   }
@@ -144,25 +201,15 @@ __device__ __forceinline__ void rows_acc(v4<A> (&acc)[MAXT], const A* At, const 
     const int tile = w + 4 * t;
     if (tile >= ntiles) break;
     const int col = 16 * tile + lr;
-    const T* y = Y + (r0 + lg) * (int64_t)D + col;
     A yv[16];
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
-      yv[s] = (((rows_ok >> s) & 1u) && col < D) ? (A)Io<T>::one(y + (int64_t)(4 * s) * D) : A(0);
+    for (int s = 0; s < 16; ++s) {
+      const bool ok = ((rows_ok >> s) & 1u) && col < D;
+      yv[s] = (A)ld_sel(Y, (r0 + lg + 4 * s) * (int64_t)D + col, ok, T(0));
+    }
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc[t] = mfma4(af[s], yv[s], acc[t]);
   }
-}
-
-__device__ __forceinline__ bool row_valid(const uint8_t* valid, int64_t b, int64_t C, int64_t row) {
-  return row < C && (!valid || valid[b * C + row] != 0);
-}
-
-__device__ __forceinline__ float inv_norm(const float* nrm, int64_t idx, float norm_eps) {
-  return 1.f / fmaxf(nrm[idx], norm_eps);
-}
-__device__ __forceinline__ double inv_norm(const double* nrm, int64_t idx, double norm_eps) {
-  return 1.0 / fmax(nrm[idx], norm_eps);
 }
 
 // Sum over the 16 lanes of a lane group (lanes sharing lg).
@@ -313,13 +360,14 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
   const T* zb = (const T*)p.z + b * C * D;
   const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
   const int64_t nkt = p.causal ? cdiv(qend, kTile) : cdiv(C, kTile);
-  const T* vt = (const T*)p.v;
+  const bool hv = p.v != nullptr;
+  const T* vt = hv ? (const T*)p.v : zb;  // stand-in when absent (see ld_sel)
 
   // A-operand rows of the row dots: query q0 + lr.
   const int64_t qa = q0 + lr;
   const bool qa_ok = row_valid(p.valid, b, C, qa);
-  const T* qa_row = qa_ok ? zb + qa * D : nullptr;
-  const A qa_inv = qa_ok ? inv_norm(ws.nrm, b * C + qa, neps) : A(0);
+  const T* qa_row = zb + (qa_ok ? qa : 0) * D;
+  const A qa_inv = inv_norm_sel(ws.nrm, b * C + qa, qa_ok, neps);
 
   // ---- pass 1: num, den ----
   v4<A> acc[MAXT];
@@ -329,14 +377,15 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * kTile + 16 * w + lr;  // this lane's key (B row, output column)
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const A k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : A(0);
-    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_inv, k_ok ? zb + k * D : nullptr, k_inv, D, vec, lg);
+    const A k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
+    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_ok, qa_inv, zb + (k_ok ? k : 0) * D, k_ok, k_inv, D, vec, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
       A pv = A(0);
-      if (m) pv = s4[i] * (vt ? (A)Io<T>::one(vt + q * C + k) : A(1));
+      const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
+      if (m) pv = s4[i] * vv;
       den4[i] += pv;
       tile[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = pv;
     }
@@ -421,18 +470,18 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * kTile + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const A k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : A(0);
-    const T* k_row = k_ok ? zb + k * D : nullptr;
-    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_inv, k_row, k_inv, D, vec, lg);
-    v4<A> d4 = row_dot<A, A, T>(dn_row, A(1), k_row, A(1), D, vec, lg);
+    const A k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
+    const T* k_row = zb + (k_ok ? k : 0) * D;
+    v4<A> s4 = row_dot<A, T, T>(qa_row, qa_ok, qa_inv, k_row, k_ok, k_inv, D, vec, lg);
+    v4<A> d4 = row_dot<A, A, T>(dn_row, true, A(1), k_row, k_ok, A(1), D, vec, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
       A dsv = A(0);
+      const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
       if (m) {
         const A dpv = d4[i] + stat[kRows + acc_row<A>(lg, i)];
-        const A vv = vt ? (A)Io<T>::one(vt + q * C + k) : A(1);
         dsv = dpv * vv * k_inv;
         if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i]);
       }
@@ -475,12 +524,13 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
   const A neps = (A)p.norm_eps;
   const T* zb = (const T*)p.z + b * C * D;
   const A* dnb = ws.dnum + b * C * D;
-  const T* vt = (const T*)p.v;
+  const bool hv = p.v != nullptr;
+  const T* vt = hv ? (const T*)p.v : zb;  // stand-in when absent (see ld_sel)
 
   const int64_t ka = k0 + lr;  // A row of the row dots: key k0 + lr
   const bool ka_ok = row_valid(p.valid, b, C, ka);
-  const T* ka_row = ka_ok ? zb + ka * D : nullptr;
-  const A ka_inv = ka_ok ? inv_norm(ws.nrm, b * C + ka, neps) : A(0);
+  const T* ka_row = zb + (ka_ok ? ka : 0) * D;
+  const A ka_inv = inv_norm_sel(ws.nrm, b * C + ka, ka_ok, neps);
 
   v4<A> acc1[MAXT], acc2[MAXT];
 #pragma unroll
@@ -490,17 +540,17 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
     const int64_t q = qt + 16 * w + lr;  // this lane's query (B row, output column)
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
-    const A q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : A(0);
-    v4<A> s4 = row_dot<A, T, T>(ka_row, ka_inv, q_ok ? zb + q * D : nullptr, q_inv, D, vec, lg);
-    v4<A> d4 = row_dot<A, T, A>(ka_row, A(1), q_in ? dnb + q * D : nullptr, A(1), D, vec, lg);
-    const A dd = q_in ? ws.dden[b * C + q] : A(0);
+    const A q_inv = inv_norm_sel(ws.nrm, b * C + q, q_ok, neps);
+    v4<A> s4 = row_dot<A, T, T>(ka_row, ka_ok, ka_inv, zb + (q_ok ? q : 0) * D, q_ok, q_inv, D, vec, lg);
+    v4<A> d4 = row_dot<A, T, A>(ka_row, ka_ok, A(1), dnb + (q_in ? q : 0) * D, q_in, A(1), D, vec, lg);
+    const A dd = ld_sel(ws.dden, b * C + q, q_in, A(0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + acc_row<A>(lg, i);
       const bool m = q_in && row_valid(p.valid, b, C, k) && (!p.causal || k <= q);
       A pv = A(0), dsv = A(0);
+      const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
       if (m) {
-        const A vv = vt ? (A)Io<T>::one(vt + q * C + k) : A(1);
         pv = s4[i] * vv;
         dsv = (d4[i] + dd) * vv * q_inv;
       }
@@ -615,10 +665,11 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 __device__ __forceinline__ bf16x8 ld8(const __bf16* p) { return *(const bf16x8*)p; }
 __device__ __forceinline__ bf16x8 zero8() { return __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u}); }
 
-// 16 x 16 block of A B^T over D features (A row lr = a, B row lr = b; a null row
-// is zero and not read). Lane group lg feeds features 32s + 8lg .. +7 at step s.
-// Loads of 8 steps are issued before their MFMAs. Result: lane holds C[4 lg + i][lr].
-__device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, int D, int lg) {
+// 16 x 16 block of A B^T over D features (A row lr = a, in LDS; B row lr = b, a row
+// of global memory that is always readable, taken as zeros where !bok). Lane group lg
+// feeds features 32s + 8lg .. +7 at step s. Loads of 8 steps are issued before their
+// MFMAs, without branches (see ld_sel). Result: lane holds C[4 lg + i][lr].
+__device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, bool bok, int D, int lg) {
   f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
   const int steps = (D + 31) >> 5;
   for (int s0 = 0; s0 < steps; s0 += 8) {
@@ -627,8 +678,9 @@ __device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, int
     for (int u = 0; u < 8; ++u) {
       const int d = 32 * (s0 + u) + 8 * lg;
       const bool in = s0 + u < steps && d < D;
-      x[u] = (a && in) ? ld8(a + d) : zero8();
-      y[u] = (b && in) ? ld8(b + d) : zero8();
+      x[u] = in ? ld8(a + d) : zero8();
+      const bf16x8 yl = ld8(b + (in ? d : 0));
+      y[u] = (bok && in) ? yl : zero8();
     }
 #pragma unroll
     for (int u = 0; u < 8; u += 2) {
@@ -639,48 +691,38 @@ __device__ __forceinline__ f32x4 row_dot16(const __bf16* a, const __bf16* b, int
   return c0 + c1;
 }
 
-// Two row dots sharing an operand: c1 = a1 b^T and c2 = a2 b^T (b loaded once), or
-// with `shared_a`, c1 = a b1^T and c2 = a b2^T (a loaded once). Same lane layout
-// as row_dot16; a null row is zero and not read.
-template <bool shared_a>
-__device__ __forceinline__ void row_dot16x2(const __bf16* a1, const __bf16* a2, const __bf16* b1, const __bf16* b2,
+// Two row dots sharing the LDS operand: c1 = a b1^T and c2 = a b2^T (a loaded once;
+// b1, b2 readable global rows, zeros where !ok1 / !ok2). Same lane layout as row_dot16.
+__device__ __forceinline__ void row_dot16x2(const __bf16* a, const __bf16* b1, bool ok1, const __bf16* b2, bool ok2,
                                             int D, int lg, f32x4& c1, f32x4& c2) {
   c1 = f32x4{0.f, 0.f, 0.f, 0.f};
   c2 = f32x4{0.f, 0.f, 0.f, 0.f};
   const int steps = (D + 31) >> 5;
   for (int s0 = 0; s0 < steps; s0 += 4) {
-    bf16x8 x1[4], x2[4], y1[4], y2[4];
+    bf16x8 x1[4], y1[4], y2[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int d = 32 * (s0 + u) + 8 * lg;
       const bool in = s0 + u < steps && d < D;
-      if (shared_a) {
-        x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
-        y1[u] = (b1 && in) ? ld8(b1 + d) : zero8();
-        y2[u] = (b2 && in) ? ld8(b2 + d) : zero8();
-      } else {
-        x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
-        x2[u] = (a2 && in) ? ld8(a2 + d) : zero8();
-        y1[u] = (b1 && in) ? ld8(b1 + d) : zero8();
-      }
+      const int dl = in ? d : 0;
+      x1[u] = in ? ld8(a + d) : zero8();
+      const bf16x8 l1 = ld8(b1 + dl), l2 = ld8(b2 + dl);
+      y1[u] = (ok1 && in) ? l1 : zero8();
+      y2[u] = (ok2 && in) ? l2 : zero8();
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      if (shared_a) {
-        c1 = mfma16(x1[u], y1[u], c1);
-        c2 = mfma16(x1[u], y2[u], c2);
-      } else {
-        c1 = mfma16(x1[u], y1[u], c1);
-        c2 = mfma16(x2[u], y1[u], c2);
-      }
+      c1 = mfma16(x1[u], y1[u], c1);
+      c2 = mfma16(x1[u], y2[u], c2);
     }
   }
 }
 
-// Three row dots sharing the right operand: c1 = a1 b^T, c2 = a2 b^T, c3 = a3 b^T (b
-// loaded once). Same lane layout as row_dot16; a null row is zero and not read.
+// Three row dots sharing the global operand: c1 = a1 b^T, c2 = a2 b^T, c3 = a3 b^T
+// (a1..a3 in LDS; b a readable global row, zeros where !bok, loaded once). Same lane
+// layout as row_dot16.
 __device__ __forceinline__ void row_dot16x3(const __bf16* a1, const __bf16* a2, const __bf16* a3, const __bf16* b,
-                                            int D, int lg, f32x4& c1, f32x4& c2, f32x4& c3) {
+                                            bool bok, int D, int lg, f32x4& c1, f32x4& c2, f32x4& c3) {
   c1 = f32x4{0.f, 0.f, 0.f, 0.f};
   c2 = f32x4{0.f, 0.f, 0.f, 0.f};
   c3 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -691,10 +733,11 @@ __device__ __forceinline__ void row_dot16x3(const __bf16* a1, const __bf16* a2, 
     for (int u = 0; u < 4; ++u) {
       const int d = 32 * (s0 + u) + 8 * lg;
       const bool in = s0 + u < steps && d < D;
-      x1[u] = (a1 && in) ? ld8(a1 + d) : zero8();
-      x2[u] = (a2 && in) ? ld8(a2 + d) : zero8();
-      x3[u] = (a3 && in) ? ld8(a3 + d) : zero8();
-      y[u] = (b && in) ? ld8(b + d) : zero8();
+      x1[u] = in ? ld8(a1 + d) : zero8();
+      x2[u] = in ? ld8(a2 + d) : zero8();
+      x3[u] = in ? ld8(a3 + d) : zero8();
+      const bf16x8 yl = ld8(b + (in ? d : 0));
+      y[u] = (bok && in) ? yl : zero8();
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -713,7 +756,9 @@ __device__ __forceinline__ void stage_rows16(__bf16* dst, int pitch, const __bf1
   for (int i = threadIdx.x; i < kRows * chunks; i += blockDim.x) {
     const int r = i / chunks, c = (i - r * chunks) * 8;
     const int64_t row = r0 + r;
-    *(bf16x8*)(dst + r * pitch + c) = row_valid(valid, b, C, row) ? ld8(zb + row * D + c) : zero8();
+    const bool ok = row_valid(valid, b, C, row);
+    const bf16x8 x = ld8(zb + (ok ? row : 0) * D + c);
+    *(bf16x8*)(dst + r * pitch + c) = ok ? x : zero8();
   }
 }
 
@@ -738,9 +783,12 @@ __device__ __forceinline__ void rows_acc16(f32x4 (&acc)[MAXT], const __bf16* A, 
     for (int t = 0; t < G; ++t) {
       const int col = 16 * (w + NW * (t0 + t)) + lr;
       const bool in = w + NW * (t0 + t) < ntiles && col < D;
-      const __bf16* yp = Yt + (int64_t)col * cp + r0 + 8 * lg;
+      const __bf16* yp = Yt + (int64_t)(in ? col : 0) * cp + r0 + 8 * lg;  // always readable (see ld_sel)
 #pragma unroll
-      for (int k = 0; k < KS; ++k) y[t][k] = in ? ld8(yp + 32 * k) : zero8();
+      for (int k = 0; k < KS; ++k) {
+        const bf16x8 l = ld8(yp + 32 * k);
+        y[t][k] = in ? l : zero8();
+      }
     }
 #pragma unroll
     for (int t = 0; t < G; ++t) {
@@ -806,7 +854,10 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
   const float neps = (float)p.norm_eps;
   const __bf16* zb = (const __bf16*)p.z + b * C * D;
   const __bf16* ztb = ws.zt + b * D * cp;
-  const __bf16* vt = (const __bf16*)p.v;
+  // Optional operands read through a stand-in pointer when absent (selected away), so
+  // that no load sits in a branch (see ld_sel).
+  const bool hv = p.v != nullptr;
+  const __bf16* vt = hv ? (const __bf16*)p.v : zb;
   const int64_t qend = q0 + kRows < C ? q0 + kRows : C;
   const int64_t nkt = p.causal ? cdiv(qend, KT) : cdiv(C, KT);
 
@@ -816,7 +867,7 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t q = q0 + 4 * lg + i;
-    qinv[i] = row_valid(p.valid, b, C, q) ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
+    qinv[i] = inv_norm_sel(ws.nrm, b * C + q, row_valid(p.valid, b, C, q), neps);
   }
 
   __syncthreads();
@@ -829,14 +880,15 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
-    const f32x4 s4 = row_dot16(qa_row, k_ok ? zb + k * D : nullptr, D, lg);
+    const float k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
+    const f32x4 s4 = row_dot16(qa_row, zb + (k_ok ? k : 0) * D, k_ok, D, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
       const bool m = k_ok && q < C && (!p.causal || k <= q);
       float pv = 0.f;
-      if (m) pv = s4[i] * qinv[i] * k_inv * (vt ? (float)vt[q * C + k] : 1.f);
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
+      if (m) pv = s4[i] * qinv[i] * k_inv * vv;
       den4[i] += pv;
       tile[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)pv;
     }
@@ -859,9 +911,33 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
   // ---- epilogue 1: dz_tl, dnum (LDS, row-major and transposed bf16), dden, dbias ----
   const int ntiles = (D + 15) >> 4;
   float ddp[4] = {0.f, 0.f, 0.f, 0.f};
-  const __bf16* gb = p.gate ? (const __bf16*)p.gate + b * C * D : nullptr;
+  const bool hg = p.gate != nullptr, hb = p.bias != nullptr;
   const __bf16* ob = (const __bf16*)p.dout + b * C * D;
+  const __bf16* gb = hg ? (const __bf16*)p.gate + b * C * D : ob;
+  const __bf16* bsp = hb ? (const __bf16*)p.bias : ob;
   __bf16* dgb = p.dgate ? (__bf16*)p.dgate + b * C * D : nullptr;
+  // Every input of the epilogue is loaded before its first store: the stores (dz_tl,
+  // dnum) may alias the inputs as far as the compiler can tell, so otherwise each
+  // element's loads wait until the previous element's stores have been issued, one
+  // memory round trip per element (38% of the heaviest workgroup's time at C2).
+  bool rqv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rqv[i] = row_valid(p.valid, b, C, q0 + 4 * lg + i);
+  float gov[MAXT][4], gtv[MAXT][4], bsv[MAXT];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    const int col = 16 * (w + NW * t) + lr;
+    const bool cin = w + NW * t < ntiles && col < D;
+    bsv[t] = (float)ld_sel(bsp, col, cin && hb, (__bf16)0.f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool ok = cin && rqv[i];
+      gov[t][i] = (float)ld_sel(ob, q * D + col, ok, (__bf16)0.f);
+      const float gl = (float)ld_sel(gb, q * D + col, ok && hg, (__bf16)0.f);
+      gtv[t][i] = hg ? gl : 1.f;
+    }
+  }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
     const int tile_i = w + NW * t;
@@ -875,12 +951,10 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
       const int64_t q = q0 + row;
       float dn = 0.f;
       if (col < D && q < C) {
-        const bool rq = row_valid(p.valid, b, C, q);
         const float den = stat[row];
         const float y = p.normalize ? acc[t][i] / den : acc[t][i];
-        const float u = y + (p.bias ? (float)((const __bf16*)p.bias)[col] : 0.f);
-        const float go = rq ? (float)ob[q * D + col] : 0.f;
-        const float gt = gb ? (rq ? (float)gb[q * D + col] : 0.f) : 1.f;
+        const float u = y + bsv[t];
+        const float go = gov[t][i], gt = gtv[t][i];
         if (dgb) dgb[q * D + col] = (__bf16)(go * activate<float>(u, p.act));
         const float du = go * gt * act_grad(u, p.act);
         dbs += du;
@@ -923,19 +997,18 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
   for (int64_t kt = 0; kt < nkt; ++kt) {
     const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
-    const float k_inv = k_ok ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
-    const __bf16* k_row = k_ok ? zb + k * D : nullptr;
+    const float k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
     f32x4 s4, d4, d4lo;
-    row_dot16x3(qa_row, dn_row, dnlo_row, k_row, D, lg, s4, d4, d4lo);
+    row_dot16x3(qa_row, dn_row, dnlo_row, zb + (k_ok ? k : 0) * D, k_ok, D, lg, s4, d4, d4lo);
     d4 += d4lo;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
       const bool m = k_ok && q < C && (!p.causal || k <= q);
       float dsv = 0.f;
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
       if (m) {
         const float dpv = d4[i] + stat[kRows + 4 * lg + i];
-        const float vv = vt ? (float)vt[q * C + k] : 1.f;
         dsv = dpv * vv * k_inv;
         if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i] * qinv[i] * k_inv);
       }
@@ -979,7 +1052,8 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
   const __bf16* ztb = ws.zt + b * D * cp;
   const __bf16* dnb = ws.dn16 + b * C * D;
   const __bf16* dntb = ws.dnt + b * D * cp;
-  const __bf16* vt = (const __bf16*)p.v;
+  const bool hv = p.v != nullptr;
+  const __bf16* vt = hv ? (const __bf16*)p.v : zb;  // stand-in when absent (see ld_sel)
 
   stage_rows16(kzl, dp, zb, p.valid, b, C, k0, D);
   const __bf16* ka_row = kzl + lr * dp;  // A rows of the row dots (zero when padded)
@@ -989,7 +1063,7 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
   for (int i = 0; i < 4; ++i) {
     const int64_t k = k0 + 4 * lg + i;
     kok[i] = row_valid(p.valid, b, C, k);
-    kinv[i] = kok[i] ? inv_norm(ws.nrm, b * C + k, neps) : 0.f;
+    kinv[i] = inv_norm_sel(ws.nrm, b * C + k, kok[i], neps);
   }
 
   __syncthreads();
@@ -1003,17 +1077,17 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
     const int64_t q = qt + 16 * w + lr;
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
-    const float q_inv = q_ok ? inv_norm(ws.nrm, b * C + q, neps) : 0.f;
+    const float q_inv = inv_norm_sel(ws.nrm, b * C + q, q_ok, neps);
     f32x4 s4, d4;
-    row_dot16x2<true>(ka_row, nullptr, q_ok ? zb + q * D : nullptr, q_in ? dnb + q * D : nullptr, D, lg, s4, d4);
-    const float dd = q_in ? ws.dden[b * C + q] : 0.f;
+    row_dot16x2(ka_row, zb + (q_ok ? q : 0) * D, q_ok, dnb + (q_in ? q : 0) * D, q_in, D, lg, s4, d4);
+    const float dd = ld_sel(ws.dden, b * C + q, q_in, 0.f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + 4 * lg + i;
       const bool m = q_in && kok[i] && (!p.causal || k <= q);
       float pv = 0.f, dsv = 0.f;
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
       if (m) {
-        const float vv = vt ? (float)vt[q * C + k] : 1.f;
         pv = s4[i] * kinv[i] * q_inv * vv;
         dsv = (d4[i] + dd) * vv * q_inv;
       }
@@ -1026,21 +1100,25 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
     __syncthreads();
   }
 
+  // The block's z values are loaded here once and kept for the dz_tr stores below, so
+  // that no load follows a store there (the compiler cannot tell dz_tr from z apart and
+  // would finish each store's round trip before the next load).
   const int ntiles = (D + 15) >> 4;
   float rp[4] = {0.f, 0.f, 0.f, 0.f};
+  float zv[MAXT][4];
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + NW * t;
-    if (tile_i >= ntiles) break;
-    const int col = 16 * tile_i + lr;
+    const int col = 16 * (w + NW * t) + lr;
+    const bool cin = w + NW * t < ntiles && col < D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + 4 * lg + i;
-      if (col < D && kok[i]) {
-        const float g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
-        acc2[t][i] = g;
-        rp[i] += (float)zb[k * D + col] * g;
-      }
+      const bool ok = cin && kok[i];
+      const float dq = ld_sel(ws.dzr, (b * C + k) * D + col, ok, 0.f);
+      zv[t][i] = (float)ld_sel(zb, k * D + col, ok, (__bf16)0.f);
+      const float g = acc2[t][i] + dq;
+      acc2[t][i] = g;
+      rp[i] += zv[t][i] * g;
     }
   }
 #pragma unroll
@@ -1072,7 +1150,7 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
       if (col >= D || k >= C) continue;
       float g = 0.f;
       if (kok[i]) {
-        const float zh = (float)zb[k * D + col] * kinv[i];
+        const float zh = zv[t][i] * kinv[i];
         g = acc1[t][i] + (acc2[t][i] - zh * rad[4 * lg + i]) * kinv[i];
       }
       dzb[k * D + col] = (__bf16)g;
