@@ -411,40 +411,68 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
   // ---- epilogue 1: dz_tl, dnum, dden, dbias ----
   const int ntiles = (D + 15) >> 4;
   A ddp[4] = {A(0), A(0), A(0), A(0)};
-  const T* gb = p.gate ? (const T*)p.gate + b * C * D : nullptr;
+  const bool hg = p.gate != nullptr, hb = p.bias != nullptr;
   const T* ob = (const T*)p.dout + b * C * D;
+  const T* gb = hg ? (const T*)p.gate + b * C * D : ob;  // stand-ins when absent (see ld_sel)
+  const T* bsp = hb ? (const T*)p.bias : ob;
   T* dgb = p.dgate ? (T*)p.dgate + b * C * D : nullptr;
+  bool rqv[4];
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
-    if (tile_i >= ntiles) break;
-    const int col = 16 * tile_i + lr;
-    A dbs = A(0);
+  for (int i = 0; i < 4; ++i) rqv[i] = row_valid(p.valid, b, C, q0 + acc_row<A>(lg, i));
+  // Four column tiles at a time, inputs loaded before the first store: the stores may
+  // alias the inputs as far as the compiler can tell, so otherwise every element's
+  // loads wait until the previous element's stores have gone out.
+  constexpr int EB = MAXT < 4 ? MAXT : 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = acc_row<A>(lg, i);
-      const int64_t q = q0 + row;
-      A dn = A(0);
-      if (col < D && q < C) {
-        const bool rq = row_valid(p.valid, b, C, q);
-        const A den = stat[row];
-        const A y = p.normalize ? acc[t][i] / den : acc[t][i];
-        const A u = y + (p.bias ? (A)Io<T>::one((const T*)p.bias + col) : A(0));
-        const A go = rq ? (A)Io<T>::one(ob + q * D + col) : A(0);
-        const A gt = gb ? (rq ? (A)Io<T>::one(gb + q * D + col) : A(0)) : A(1);
-        if (dgb) Io<T>::put(dgb + q * D + col, (float)(go * activate<A>(u, p.act)));
-        const A du = go * gt * act_grad(u, p.act);
-        dbs += du;
-        dn = p.normalize ? du / den : du;
-        ddp[i] += du * y;
-        ws.dnum[(b * C + q) * D + col] = dn;
+  for (int t0 = 0; t0 < MAXT; t0 += EB) {
+    if (w + 4 * t0 >= ntiles) break;
+    float gov[EB][4], gtv[EB][4], bsv[EB];
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      const int col = 16 * (w + 4 * (t0 + e)) + lr;
+      const bool cin = w + 4 * (t0 + e) < ntiles && col < D;
+      bsv[e] = (float)ld_sel(bsp, col, cin && hb, T(0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t q = q0 + acc_row<A>(lg, i);
+        const bool ok = cin && rqv[i];
+        gov[e][i] = (float)ld_sel(ob, q * D + col, ok, T(0));
+        const float gl = (float)ld_sel(gb, q * D + col, ok && hg, T(0));
+        gtv[e][i] = hg ? gl : 1.f;
       }
-      dnl[row * dp + col] = dn;
     }
-    if (ws.db) {
-      dbs += __shfl_xor(dbs, 16);
-      dbs += __shfl_xor(dbs, 32);
-      if (lg == 0 && col < D) unsafeAtomicAdd(ws.db + col, dbs);
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      const int t = t0 + e;
+      const int tile_i = w + 4 * t;
+      if (tile_i >= ntiles) break;
+      const int col = 16 * tile_i + lr;
+      A dbs = A(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = acc_row<A>(lg, i);
+        const int64_t q = q0 + row;
+        A dn = A(0);
+        if (col < D && q < C) {
+          const A den = stat[row];
+          const A y = p.normalize ? acc[t][i] / den : acc[t][i];
+          const A u = y + (A)bsv[e];
+          const A go = (A)gov[e][i];
+          const A gt = (A)gtv[e][i];
+          if (dgb) Io<T>::put(dgb + q * D + col, (float)(go * activate<A>(u, p.act)));
+          const A du = go * gt * act_grad(u, p.act);
+          dbs += du;
+          dn = p.normalize ? du / den : du;
+          ddp[i] += du * y;
+          ws.dnum[(b * C + q) * D + col] = dn;
+        }
+        dnl[row * dp + col] = dn;
+      }
+      if (ws.db) {
+        dbs += __shfl_xor(dbs, 16);
+        dbs += __shfl_xor(dbs, 32);
+        if (lg == 0 && col < D) unsafeAtomicAdd(ws.db + col, dbs);
+      }
     }
   }
 #pragma unroll
@@ -570,8 +598,18 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
     __syncthreads();
   }
 
-  // Epilogue: dzhat = key-side + query-side parts; J; row mask.
+  // Epilogue: dzhat = key-side + query-side parts; J; row mask. Loads are branch-free
+  // (see ld_sel), and the stores go out four column tiles at a time after that group's
+  // loads (the compiler cannot tell dz_tr from z apart).
   const int ntiles = (D + 15) >> 4;
+  bool kv[4];
+  A kinv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t k = k0 + acc_row<A>(lg, i);
+    kv[i] = row_valid(p.valid, b, C, k);
+    kinv[i] = inv_norm_sel(ws.nrm, b * C + k, kv[i], neps);
+  }
   A rp[4] = {A(0), A(0), A(0), A(0)};
 #pragma unroll
   for (int t = 0; t < MAXT; ++t) {
@@ -581,10 +619,13 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + acc_row<A>(lg, i);
-      if (col < D && row_valid(p.valid, b, C, k)) {
-        const A g = acc2[t][i] + ws.dzr[(b * C + k) * D + col];
+      const bool ok = col < D && kv[i];
+      const A dq = ld_sel(ws.dzr, (b * C + k) * D + col, ok, A(0));
+      const A zv = (A)ld_sel(zb, k * D + col, ok, T(0));
+      if (ok) {
+        const A g = acc2[t][i] + dq;
         acc2[t][i] = g;
-        rp[i] += (A)Io<T>::one(zb + k * D + col) * g;
+        rp[i] += zv * g;
       }
     }
   }
@@ -607,22 +648,36 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
   }
   __syncthreads();
   T* dzb = (T*)p.dz + b * C * D;
+  constexpr int EB = MAXT < 4 ? MAXT : 4;
 #pragma unroll
-  for (int t = 0; t < MAXT; ++t) {
-    const int tile_i = w + 4 * t;
-    if (tile_i >= ntiles) break;
-    const int col = 16 * tile_i + lr;
+  for (int t0 = 0; t0 < MAXT; t0 += EB) {
+    if (w + 4 * t0 >= ntiles) break;
+    float zv[EB][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t k = k0 + acc_row<A>(lg, i);
-      if (col >= D || k >= C) continue;
-      A g = A(0);
-      if (row_valid(p.valid, b, C, k)) {
-        const A inv = inv_norm(ws.nrm, b * C + k, neps);
-        const A zh = (A)Io<T>::one(zb + k * D + col) * inv;
-        g = acc1[t][i] + (acc2[t][i] - zh * rad[acc_row<A>(lg, i)]) * inv;
+    for (int e = 0; e < EB; ++e) {
+      const int col = 16 * (w + 4 * (t0 + e)) + lr;
+      const bool cin = w + 4 * (t0 + e) < ntiles && col < D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        zv[e][i] = (float)ld_sel(zb, (k0 + acc_row<A>(lg, i)) * D + col, cin && kv[i], T(0));
+    }
+#pragma unroll
+    for (int e = 0; e < EB; ++e) {
+      const int t = t0 + e;
+      const int tile_i = w + 4 * t;
+      if (tile_i >= ntiles) break;
+      const int col = 16 * tile_i + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t k = k0 + acc_row<A>(lg, i);
+        if (col >= D || k >= C) continue;
+        A g = A(0);
+        if (kv[i]) {
+          const A zh = (A)zv[e][i] * kinv[i];
+          g = acc1[t][i] + (acc2[t][i] - zh * rad[acc_row<A>(lg, i)]) * kinv[i];
+        }
+        Io<T>::put(dzb + k * D + col, (float)g);
       }
-      Io<T>::put(dzb + k * D + col, (float)g);
     }
   }
 }
