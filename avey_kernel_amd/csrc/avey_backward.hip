@@ -383,9 +383,8 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      A pv = A(0);
       const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
-      if (m) pv = s4[i] * vv;
+      const A pv = m ? s4[i] * vv : A(0);  // a select: a use inside `if (m)` sinks the load there
       den4[i] += pv;
       tile[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = pv;
     }
@@ -506,13 +505,10 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(BwdParams p, WsT<A> ws) {
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + acc_row<A>(lg, i);
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      A dsv = A(0);
       const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
-      if (m) {
-        const A dpv = d4[i] + stat[kRows + acc_row<A>(lg, i)];
-        dsv = dpv * vv * k_inv;
-        if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i]);
-      }
+      const A dpv = d4[i] + stat[kRows + acc_row<A>(lg, i)];
+      const A dsv = m ? dpv * vv * k_inv : A(0);
+      if (m && ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i]);
       tile[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = dsv;
     }
     uint32_t rows_ok = 0;
@@ -576,12 +572,9 @@ __global__ __launch_bounds__(256) void bwd_cols_kernel(BwdParams p, WsT<A> ws) {
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + acc_row<A>(lg, i);
       const bool m = q_in && row_valid(p.valid, b, C, k) && (!p.causal || k <= q);
-      A pv = A(0), dsv = A(0);
       const A vl = (A)ld_sel(vt, q * C + k, m && hv, T(0)), vv = hv ? vl : A(1);
-      if (m) {
-        pv = s4[i] * vv;
-        dsv = (d4[i] + dd) * vv * q_inv;
-      }
+      const A pv = m ? s4[i] * vv : A(0);
+      const A dsv = m ? (d4[i] + dd) * vv * q_inv : A(0);
       pt[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = pv;
       dt[acc_row<A>(lg, i) * kPitch + 16 * w + lr] = dsv;
     }
@@ -936,14 +929,22 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
     const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
+    // V's words go out ahead of the row dot, and P is formed with selects: a use inside
+    // `if (m)` lets the compiler sink each load into its branch and wait there.
+    float vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f);
+      vv[i] = hv ? vl : 1.f;
+    }
     const f32x4 s4 = row_dot16(qa_row, zb + (k_ok ? k : 0) * D, k_ok, D, lg);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      float pv = 0.f;
-      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
-      if (m) pv = s4[i] * qinv[i] * k_inv * vv;
+      const float pv = m ? s4[i] * qinv[i] * k_inv * vv[i] : 0.f;
       den4[i] += pv;
       tile[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)pv;
     }
@@ -1053,6 +1054,14 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
     const int64_t k = kt * KT + 16 * w + lr;
     const bool k_ok = row_valid(p.valid, b, C, k);
     const float k_inv = inv_norm_sel(ws.nrm, b * C + k, k_ok, neps);
+    float vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t q = q0 + 4 * lg + i;
+      const bool m = k_ok && q < C && (!p.causal || k <= q);
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f);
+      vv[i] = hv ? vl : 1.f;
+    }
     f32x4 s4, d4, d4lo;
     row_dot16x3(qa_row, dn_row, dnlo_row, zb + (k_ok ? k : 0) * D, k_ok, D, lg, s4, d4, d4lo);
     d4 += d4lo;
@@ -1060,13 +1069,9 @@ __global__ __launch_bounds__(64 * NW) void bwd16_rows_kernel(BwdParams p, Ws ws)
     for (int i = 0; i < 4; ++i) {
       const int64_t q = q0 + 4 * lg + i;
       const bool m = k_ok && q < C && (!p.causal || k <= q);
-      float dsv = 0.f;
-      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
-      if (m) {
-        const float dpv = d4[i] + stat[kRows + 4 * lg + i];
-        dsv = dpv * vv * k_inv;
-        if (ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i] * qinv[i] * k_inv);
-      }
+      const float dpv = d4[i] + stat[kRows + 4 * lg + i];
+      const float dsv = m ? dpv * vv[i] * k_inv : 0.f;
+      if (m && ws.dv) unsafeAtomicAdd(ws.dv + q * C + k, dpv * s4[i] * qinv[i] * k_inv);
       tile[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)dsv;
     }
     __syncthreads();
@@ -1133,19 +1138,23 @@ __global__ __launch_bounds__(64 * NW) void bwd16_cols_kernel(BwdParams p, Ws ws)
     const bool q_in = q < C;
     const bool q_ok = row_valid(p.valid, b, C, q);
     const float q_inv = inv_norm_sel(ws.nrm, b * C + q, q_ok, neps);
-    f32x4 s4, d4;
-    row_dot16x2(ka_row, zb + (q_ok ? q : 0) * D, q_ok, dnb + (q_in ? q : 0) * D, q_in, D, lg, s4, d4);
-    const float dd = ld_sel(ws.dden, b * C + q, q_in, 0.f);
+    float vv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t k = k0 + 4 * lg + i;
       const bool m = q_in && kok[i] && (!p.causal || k <= q);
-      float pv = 0.f, dsv = 0.f;
-      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f), vv = hv ? vl : 1.f;
-      if (m) {
-        pv = s4[i] * kinv[i] * q_inv * vv;
-        dsv = (d4[i] + dd) * vv * q_inv;
-      }
+      const float vl = (float)ld_sel(vt, q * C + k, m && hv, (__bf16)0.f);
+      vv[i] = hv ? vl : 1.f;
+    }
+    const float dd = ld_sel(ws.dden, b * C + q, q_in, 0.f);
+    f32x4 s4, d4;
+    row_dot16x2(ka_row, zb + (q_ok ? q : 0) * D, q_ok, dnb + (q_in ? q : 0) * D, q_in, D, lg, s4, d4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t k = k0 + 4 * lg + i;
+      const bool m = q_in && kok[i] && (!p.causal || k <= q);
+      const float pv = m ? s4[i] * kinv[i] * q_inv * vv[i] : 0.f;
+      const float dsv = m ? (d4[i] + dd) * vv[i] * q_inv : 0.f;
       pt[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)pv;
       dt[(4 * lg + i) * TP + 16 * w + lr] = (__bf16)dsv;
     }
