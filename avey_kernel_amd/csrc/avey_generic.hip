@@ -72,7 +72,19 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     const int64_t q = q0 + t;
     rq[t] = q < C ? inv[q] : A(0);
   }
-  auto row_ok = [&](int64_t r) { return r < C && (!vb || vb[r]); };
+  // Guarded loads are written without branches: the load always goes out (to element 0
+  // when the guard is false) and the value is selected, so a group of loads shares one
+  // wait instead of each sitting in a branch that waits for it.
+  auto row_ok = [&](int64_t r) {
+    const bool in = r < C;
+    return vb ? (in & (vb[in ? r : 0] != 0)) : in;
+  };
+  auto ldz = [&](bool ok, int64_t idx) -> A {
+    const A x = Elem<T>::to_acc(zb[ok ? idx : 0]);
+    return ok ? x : A(0);
+  };
+  const bool hv = vw != nullptr;
+  const T* vwp = hv ? vw : zb;  // stand-in when V is absent
   const bool small = D <= DC;  // one feature chunk (C1's shape)
 
   const int64_t nkt = key_tiles_for(qt, C, BQ, BK, p.causal != 0);
@@ -82,10 +94,11 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     // key inverse norm are loaded while the current tile is used, so a tile waits on
     // no global-load round trip. Same arithmetic in the same order as below.
     static_assert(BF == DC && BK * DC % 256 == 0, "key rows serve the mixing");
-    for (int e = t; e < BQ * DC; e += 256) {
-      const int r = e / DC, c = e % DC;
+#pragma unroll
+    for (int i = 0; i < BQ * DC / 256; ++i) {
+      const int e = t + 256 * i, r = e / DC, c = e % DC;
       const int64_t q = q0 + r;
-      qs[r][c] = (c < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * p.zrs + c]) : A(0);
+      qs[r][c] = ldz(c < D && row_ok(q), q * p.zrs + c);
     }
     constexpr int KE = BK * DC / 256;  // key-row elements per thread
     A kr[KE];
@@ -94,7 +107,7 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
       for (int i = 0; i < KE; ++i) {
         const int e = t + 256 * i, r = e / DC, c = e % DC;
         const int64_t k = k0 + r;
-        kr[i] = (c < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + c]) : A(0);
+        kr[i] = ldz(c < D && row_ok(k), k * p.zrs + c);
       }
     };
     load_keys(0);
@@ -102,8 +115,8 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
       const int64_t k0 = kt * BK;
       const int64_t q = q0 + si, k = k0 + sj;
       const bool allowed = row_ok(q) && row_ok(k) && (!p.causal || k <= q);
-      const A ik = allowed ? inv[k] : A(0);
-      const A vv = (allowed && vw) ? Elem<T>::to_acc(vw[q * C + k]) : A(1);
+      const A ikl = inv[allowed ? k : 0], ik = allowed ? ikl : A(0);
+      const A vl = Elem<T>::to_acc(vwp[allowed && hv ? q * C + k : 0]), vv = hv ? vl : A(1);
       __syncthreads();  // the previous tile's reads of ks and ss are done
 #pragma unroll
       for (int i = 0; i < KE; ++i) ks[(t + 256 * i) / DC][(t + 256 * i) % DC] = kr[i];
@@ -112,12 +125,7 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
       A s = A(0);
 #pragma unroll 8
       for (int c = 0; c < DC; ++c) s += qs[si][c] * ks[sj][c];
-      if (allowed) {
-        s = s * rq[si] * ik;
-        if (vw) s *= vv;
-      } else {
-        s = A(0);
-      }
+      s = allowed ? (hv ? s * rq[si] * ik * vv : s * rq[si] * ik) : A(0);
       ss[si][sj] = s;
       __syncthreads();
       if (p.normalize && t < BQ) {
@@ -137,12 +145,13 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     A s = A(0);
     for (int64_t d0 = 0; d0 < D; d0 += DC) {
       __syncthreads();
-      for (int e = t; e < BQ * DC; e += 256) {
-        const int r = e / DC, c = e % DC;
+#pragma unroll
+      for (int i = 0; i < BQ * DC / 256; ++i) {
+        const int e = t + 256 * i, r = e / DC, c = e % DC;
         const int64_t f = d0 + c;
         const int64_t q = q0 + r, k = k0 + r;
-        qs[r][c] = (f < D && row_ok(q)) ? Elem<T>::to_acc(zb[q * p.zrs + f]) : A(0);
-        ks[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + f]) : A(0);
+        qs[r][c] = ldz(f < D && row_ok(q), q * p.zrs + f);
+        ks[r][c] = ldz(f < D && row_ok(k), k * p.zrs + f);
       }
       __syncthreads();
 #pragma unroll 8
@@ -151,18 +160,16 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
     {
       const int64_t q = q0 + si, k = k0 + sj;
       const bool allowed = row_ok(q) && row_ok(k) && (!p.causal || k <= q);
-      if (allowed) {
-        s = s * rq[si] * inv[k];
-        if (vw) s *= Elem<T>::to_acc(vw[q * C + k]);
-      } else {
-        s = A(0);
-      }
+      const A ik = inv[allowed ? k : 0];
+      const A vv = Elem<T>::to_acc(vwp[allowed && hv ? q * C + k : 0]);
+      s = allowed ? (hv ? s * rq[si] * ik * vv : s * rq[si] * ik) : A(0);
       ss[si][sj] = s;
     }
-    for (int e = t; e < BK * BF; e += 256) {
-      const int r = e / BF, c = e % BF;
+#pragma unroll
+    for (int i = 0; i < BK * BF / 256; ++i) {
+      const int e = t + 256 * i, r = e / BF, c = e % BF;
       const int64_t k = k0 + r, f = f0 + c;
-      kf[r][c] = (f < D && row_ok(k)) ? Elem<T>::to_acc(zb[k * p.zrs + f]) : A(0);
+      kf[r][c] = ldz(f < D && row_ok(k), k * p.zrs + f);
     }
     __syncthreads();
     if (p.normalize && t < BQ) {
@@ -180,19 +187,33 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(FwdParams p) {
 
   const int64_t q = q0 + oi;
   if (q >= C) return;
-  const bool qv = !vb || vb[q];
+  const bool qv = row_ok(q);
   const T* bias = (const T*)p.bias;
   const T* gate = (const T*)p.gate;
   T* out = (T*)p.out + (b * C + q) * D;
   const A dd = p.normalize ? den_s[oi] + (A)p.eps : A(1);
+  // Bias and gate words first: the output stores may alias them as far as the compiler
+  // can tell, so loads after a store would wait for it.
+  const T* biasp = bias ? bias : zb;
+  const T* gatep = gate ? gate + b * p.gbs + q * p.grs : zb;
+  A bv[4], gv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t f = f0 + of + u;
+    const bool fin = f < D;
+    const A bl = Elem<T>::to_acc(biasp[fin && bias ? f : 0]);
+    const A gl = Elem<T>::to_acc(gatep[fin && gate ? f : 0]);
+    bv[u] = bias ? bl : A(0);
+    gv[u] = gate ? (qv ? gl : A(0)) : A(1);
+  }
   for (int u = 0; u < 4; ++u) {
     const int64_t f = f0 + of + u;
     if (f >= D) break;
     A y = acc[u];
     if (p.normalize) y = y / dd;
-    if (bias) y += Elem<T>::to_acc(bias[f]);
+    if (bias) y += bv[u];
     y = activate<A>(y, p.act);
-    if (gate) y *= qv ? Elem<T>::to_acc(gate[b * p.gbs + q * p.grs + f]) : A(0);
+    if (gate) y *= gv[u];
     out[f] = Elem<T>::from_acc(qv ? y : A(0));
   }
 }
